@@ -1,0 +1,407 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+Headline (BASELINE.json metric "decode-attn HBM GB/s (% of peak) @32K ctx;
+prefill-attn TFLOPS @8K tokens"):
+  value      = Flash-Decode HBM throughput at L = 32768 (config C3), one query
+               token, 16 query heads / 4 KV heads / head_dim 128, algorithmic
+               bytes 2048*L + 8192 per call, KV rotated over 8 buffers
+               (8 x 67 MB > 256 MB Infinity Cache) so every call streams HBM.
+  prefill    = causal prefill TFLOPS at N = 8192 (config C4), algorithmic
+               FLOPs 4096*N*(N+1).
+A "step" is one decode-attention call over one KV buffer.  The K timed steps
+are one HIP-graph replay of K captured decode launches (the engine's decode
+also replays a graph, model_inference.hpp:96-126), bracketed by
+torch.cuda.synchronize() and HIP events on the launch stream.
+
+Also reported: every C3 length warm and cold, C1/C2, RoPE+append at 8192
+tokens, the 36-layer attention-only decode step C5 (72 graph nodes), and CPU
+baselines timed on this host: the oracle (fp64 C restatement, 1 thread) and
+the reference's PyTorch CPU attention (python/reference.py:61-96 restated with
+torch SDPA, fp16).  Inputs are seeded synthetic N(0, sigma) tensors.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import platform
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "llm-inference_amd" / "python"))
+
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, GB/s
+PEAK_FP16_TFLOPS = 2500.0      # MI355X dense fp16 MFMA, TFLOP/s
+HQ, HKV, D = 16, 4, 128
+Q_DIM, KV_DIM, QKV = HQ * D, HKV * D, HQ * D + 2 * HKV * D
+THETA = 5.0e6
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def decode_bytes(L):
+    return 2 * L * HKV * D * 2 + 2 * HQ * D * 2
+
+
+def prefill_flops(N):
+    return 2 * HQ * D * N * (N + 1)
+
+
+def rope_bytes(N, rotate=True):
+    return (12544 if rotate else 4096) * N
+
+
+def rand16(torch, n, seed, sigma=1.0, device="cuda"):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return (torch.randn(n, generator=g, device=device) * sigma).to(torch.float16)
+
+
+def time_graph(torch, A, hipgraph, launch_one, steps, warmup, stream):
+    """Warm up with `warmup` eager launches, capture `steps` launches into one
+    graph, replay it once inside synchronize + event brackets.  Returns ms per
+    launch."""
+    sp = stream.cuda_stream
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            launch_one(i, sp)
+        torch.cuda.synchronize()
+        hipgraph.begin_capture(sp)
+        for i in range(steps):
+            launch_one(warmup + i, sp)
+        graph, exe = hipgraph.end_capture(sp)
+        # one untimed replay so the graph's first-launch costs stay outside
+        hipgraph.launch(exe, sp)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        hipgraph.launch(exe, sp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    hipgraph.destroy(graph, exe)
+    return e0.elapsed_time(e1) / steps
+
+
+def bench_decode(torch, A, hipgraph, L, nbuf, steps, warmup, seed=3):
+    """Flash-Decode over `nbuf` distinct KV buffers in rotation."""
+    dev = torch.device("cuda:0")
+    q = rand16(torch, Q_DIM, seed)
+    ks = [rand16(torch, (L + 1) * KV_DIM, seed + 1 + 2 * b) for b in range(nbuf)]
+    vs = [rand16(torch, (L + 1) * KV_DIM, seed + 2 + 2 * b) for b in range(nbuf)]
+    po, pm, ps = A.decode_workspace(HQ, L, D, device=dev)
+    out = torch.empty(Q_DIM, dtype=torch.float16, device=dev)
+    lib = A.lib()
+    args = [(q.data_ptr(), ks[b].data_ptr(), vs[b].data_ptr(), out.data_ptr(), po.data_ptr(),
+             pm.data_ptr(), ps.data_ptr()) for b in range(nbuf)]
+
+    def launch(i, sp):
+        a = args[i % nbuf]
+        rc = lib.attn_decode(*a, 1, L, L - 1, HQ, HKV, D, QKV, KV_DIM, sp, None, None)
+        assert rc == 0
+
+    stream = torch.cuda.Stream()
+    ms = time_graph(torch, A, hipgraph, launch, steps, warmup, stream)
+    del ks, vs
+    return ms
+
+
+def bench_prefill(torch, A, N, steps, warmup, seed=4, sigma=0.5):
+    dev = torch.device("cuda:0")
+    qkv = rand16(torch, N * QKV, seed, sigma)
+    kc = rand16(torch, N * KV_DIM, seed + 1, sigma)
+    vc = rand16(torch, N * KV_DIM, seed + 2, sigma)
+    out = torch.empty(N * Q_DIM, dtype=torch.float16, device=dev)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        A.prefill(qkv, kc, vc, out, N, HQ, HKV, D, QKV, KV_DIM)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        A.prefill(qkv, kc, vc, out, N, HQ, HKV, D, QKV, KV_DIM)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def bench_rope(torch, A, hipgraph, N, nbuf, steps, warmup, rotate=True, seed=6):
+    dev = torch.device("cuda:0")
+    cos, sin = A.rope_tables(N + 1, D, THETA)
+    dcos, dsin = cos.to(dev), sin.to(dev)
+    srcs = [rand16(torch, N * QKV, seed + b) for b in range(nbuf)]
+    caches = [torch.empty(2 * N * KV_DIM, dtype=torch.float16, device=dev) for _ in range(nbuf)]
+    lib = A.lib()
+
+    def launch(i, sp):
+        s, c = srcs[i % nbuf].data_ptr(), caches[i % nbuf].data_ptr()
+        rc = lib.attn_rope_store_kv(s, s + 2 * Q_DIM, s + 2 * (Q_DIM + KV_DIM), c,
+                                    c + 2 * N * KV_DIM, dcos.data_ptr(), dsin.data_ptr(), N, HQ,
+                                    HKV, D, QKV, QKV, 0, 1 if rotate else 0, sp)
+        assert rc == 0
+
+    stream = torch.cuda.Stream()
+    return time_graph(torch, A, hipgraph, launch, steps, warmup, stream)
+
+
+def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769):
+    """36-layer attention-only decode step: per layer RoPE(+append) of one new
+    token at position L-1 (NoPE on every 4th layer, model_inference.hpp:358)
+    and Flash-Decode over L keys, captured as one 72-node graph."""
+    dev = torch.device("cuda:0")
+    S = L
+    cache = torch.empty(layers * 2 * S * KV_DIM, dtype=torch.float16, device=dev)
+    g = torch.Generator(device=dev)
+    for l in range(layers):
+        g.manual_seed(500 + l)
+        o = l * 2 * S * KV_DIM
+        cache[o:o + 2 * S * KV_DIM].normal_(generator=g)
+    qkv = torch.randn(layers, QKV, device=dev).to(torch.float16)
+    cos, sin = A.rope_tables(S, D, THETA)
+    dcos, dsin = cos.to(dev), sin.to(dev)
+    po, pm, ps = A.decode_workspace(HQ, L, D, device=dev)
+    out = torch.empty(layers, Q_DIM, dtype=torch.float16, device=dev)
+    lib = A.lib()
+    cb = cache.data_ptr()
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    start_pos = L - 1
+
+    def enqueue():
+        for l in range(layers):
+            s = qkv[l].data_ptr()
+            kc = cb + 2 * (l * 2 * S * KV_DIM)
+            vc = kc + 2 * S * KV_DIM
+            rc = lib.attn_rope_store_kv(s, s + 2 * Q_DIM, s + 2 * (Q_DIM + KV_DIM), kc, vc,
+                                        dcos.data_ptr(), dsin.data_ptr(), 1, HQ, HKV, D, QKV,
+                                        QKV, start_pos, 1 if (l + 1) % 4 != 0 else 0, sp)
+            assert rc == 0
+            rc = lib.attn_decode(s, kc, vc, out[l].data_ptr(), po.data_ptr(), pm.data_ptr(),
+                                 ps.data_ptr(), 1, L, start_pos, HQ, HKV, D, QKV, KV_DIM, sp,
+                                 None, None)
+            assert rc == 0
+
+    with torch.cuda.stream(stream):
+        hipgraph.begin_capture(sp)
+        enqueue()
+        graph, exe = hipgraph.end_capture(sp)
+        hipgraph.launch(exe, sp)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(replays):
+            hipgraph.launch(exe, sp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    hipgraph.destroy(graph, exe)
+    ms = e0.elapsed_time(e1) / replays
+    nrot = sum(1 for l in range(layers) if (l + 1) % 4 != 0)
+    byts = layers * decode_bytes(L) + nrot * rope_bytes(1, True) + (layers - nrot) * rope_bytes(1, False)
+    del cache
+    return ms, byts
+
+
+def cpu_baselines(torch, quick):
+    """Oracle (fp64 C, 1 thread) on a bounded decode sample and the reference's
+    PyTorch CPU attention (fp16 SDPA, all torch threads)."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    res = {}
+    L = 32768
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal(Q_DIM).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal(L * KV_DIM).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal(L * KV_DIM).astype(np.float16).view(np.uint16)
+    calls = 2 if quick else 8
+    oracle.attention(q, k, v, 1, HQ, HKV, D, Q_DIM, KV_DIM, L, L - 1, causal=False)
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        oracle.attention(q, k, v, 1, HQ, HKV, D, Q_DIM, KV_DIM, L, L - 1, causal=False)
+    dt = (time.perf_counter() - t0) / calls
+    res["oracle"] = {"value": decode_bytes(L) / dt / 1e9, "unit": "GB/s", "cores": 1,
+                     "kind": "port",
+                     "sample": f"{calls} Flash-Decode calls at L=32768 (16 q / 4 kv heads, D=128) "
+                               f"through the fp64 C oracle, {dt * 1e3:.1f} ms each"}
+    # reference PyTorch CPU attention (python/reference.py:79-92), fp16
+    import torch.nn.functional as F
+    nthreads = torch.get_num_threads()
+    qt = torch.from_numpy(q.view(np.float16)).view(1, HQ, 1, D)
+    kt = torch.from_numpy(k.view(np.float16)).view(1, L, HKV, D).transpose(1, 2)
+    vt = torch.from_numpy(v.view(np.float16)).view(1, L, HKV, D).transpose(1, 2)
+
+    def dec():
+        kk = kt.repeat_interleave(HQ // HKV, dim=1)
+        vv = vt.repeat_interleave(HQ // HKV, dim=1)
+        return F.scaled_dot_product_attention(qt, kk, vv)
+
+    dec()
+    times = []
+    for _ in range(3 if quick else 5):
+        t0 = time.perf_counter()
+        dec()
+        times.append(time.perf_counter() - t0)
+    dt = float(np.median(times))
+    res["torch_decode"] = {"value": decode_bytes(L) / dt / 1e9, "unit": "GB/s",
+                           "cores": nthreads, "kind": "reference-pytorch",
+                           "sample": f"torch SDPA fp16 decode L=32768, median of {len(times)}: "
+                                     f"{dt * 1e3:.2f} ms"}
+    # prefill sample: one GQA group (4 q heads, 1 kv head) at N = 8192 -> scaled
+    N = 2048 if quick else 8192
+    qp = torch.randn(1, 4, N, D).to(torch.float16)
+    kp = torch.randn(1, 1, N, D).to(torch.float16).repeat_interleave(4, dim=1)
+    vp = torch.randn(1, 1, N, D).to(torch.float16).repeat_interleave(4, dim=1)
+    t0 = time.perf_counter()
+    F.scaled_dot_product_attention(qp, kp, vp, is_causal=True)
+    dt = time.perf_counter() - t0
+    flops = 2 * 4 * D * N * (N + 1)
+    res["torch_prefill"] = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": nthreads,
+                            "kind": "reference-pytorch",
+                            "sample": f"torch SDPA fp16 causal prefill, N={N}, 4 q heads of one "
+                                      f"KV group (1/4 of C4), {dt:.2f} s"}
+    res["host"] = {"cpu_count": os.cpu_count(), "torch_threads": nthreads,
+                   "cpu": platform.processor() or platform.machine(),
+                   "torch": torch.__version__}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    res["host"]["cpu"] = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline only, short CPU sample")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the attention hot path is "
+                                   "single-device (see DESIGN.md, sharding section); run with "
+                                   "--gpus 1"}))
+        sys.exit(2)
+
+    import torch
+    import attn_mi355x as A
+    from attn_mi355x import hipgraph
+    A.lib()
+    props = torch.cuda.get_device_properties(0)
+    log(f"device {props.name} {props.gcnArchName} CUs={props.multi_processor_count}")
+    steps, warmup = args.steps, args.warmup
+
+    # ---- headline: C3 decode at L=32768, cold (8 rotated KV buffers)
+    L = 32768
+    plan = A.decode_plan(L, HQ, HKV, D, KV_DIM)
+    ms = bench_decode(torch, A, hipgraph, L, 8, steps, warmup)
+    gbs = decode_bytes(L) / (ms * 1e-3) / 1e9
+    log(f"decode L={L} cold: {ms * 1e3:.2f} us  {gbs:.0f} GB/s  ({100 * gbs / PEAK_HBM_GBS:.1f}% of peak)"
+        f" plan={plan}")
+    detail = {"decode": {}}
+    detail["decode"][str(L)] = {"cold_us": ms * 1e3, "cold_GBps": gbs, "plan": plan}
+
+    # ---- C4 prefill at 8192 tokens
+    N = 8192
+    pf_steps = max(5, min(50, steps // 4))
+    pms = bench_prefill(torch, A, N, pf_steps, 3)
+    tflops = prefill_flops(N) / (pms * 1e-3) / 1e12
+    log(f"prefill N={N}: {pms * 1e3:.1f} us  {tflops:.1f} TFLOP/s ({100 * tflops / PEAK_FP16_TFLOPS:.1f}% of fp16 peak)")
+
+    if not args.quick:
+        for Lx in (254, 4096, 16384, 32768, 65536):
+            nb = 8 if Lx >= 4096 else 1
+            cold = bench_decode(torch, A, hipgraph, Lx, nb, steps, warmup)
+            warm = bench_decode(torch, A, hipgraph, Lx, 1, steps, warmup)
+            ent = detail["decode"].setdefault(str(Lx), {})
+            ent.update({"cold_us": cold * 1e3, "cold_GBps": decode_bytes(Lx) / cold / 1e6,
+                        "warm_us": warm * 1e3, "warm_GBps": decode_bytes(Lx) / warm / 1e6,
+                        "plan": A.decode_plan(Lx, HQ, HKV, D, KV_DIM)})
+            log(f"decode L={Lx}: cold {cold * 1e3:.2f} us ({decode_bytes(Lx) / cold / 1e6:.0f} GB/s)"
+                f" warm {warm * 1e3:.2f} us ({decode_bytes(Lx) / warm / 1e6:.0f} GB/s)")
+        p254 = bench_prefill(torch, A, 254, 50, 5, sigma=1.0)
+        detail["prefill"] = {"8192": {"us": pms * 1e3, "TFLOPs": tflops},
+                             "254": {"us": p254 * 1e3,
+                                     "TFLOPs": prefill_flops(254) / p254 / 1e9}}
+        log(f"prefill N=254: {p254 * 1e3:.1f} us")
+        r8k = bench_rope(torch, A, hipgraph, 8192, 4, max(20, steps // 4), 5)
+        r254 = bench_rope(torch, A, hipgraph, 254, 1, steps, warmup)
+        r1 = bench_rope(torch, A, hipgraph, 1, 1, steps, warmup)
+        detail["rope_append"] = {
+            "8192": {"us": r8k * 1e3, "GBps": rope_bytes(8192) / r8k / 1e6},
+            "254": {"us": r254 * 1e3, "GBps": rope_bytes(254) / r254 / 1e6},
+            "1": {"us": r1 * 1e3}}
+        log(f"rope+append N=8192: {r8k * 1e3:.2f} us ({rope_bytes(8192) / r8k / 1e6:.0f} GB/s); "
+            f"N=254 {r254 * 1e3:.2f} us; N=1 {r1 * 1e3:.2f} us")
+        c5ms, c5b = bench_c5(torch, A, hipgraph, 10)
+        detail["c5_36_layer_step"] = {"us": c5ms * 1e3, "bytes": c5b,
+                                      "GBps": c5b / c5ms / 1e6,
+                                      "pct_of_hbm_peak": 100 * c5b / c5ms / 1e6 / PEAK_HBM_GBS}
+        log(f"C5 36-layer decode step: {c5ms * 1e3:.1f} us ({c5b / c5ms / 1e6:.0f} GB/s)")
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baselines ...")
+        cpu = cpu_baselines(torch, args.quick)
+        detail["cpu"] = cpu
+        log(f"CPU oracle decode {cpu['oracle']['value']:.2f} GB/s; torch CPU decode "
+            f"{cpu['torch_decode']['value']:.2f} GB/s; torch CPU prefill "
+            f"{cpu['torch_prefill']['value']:.3f} TFLOP/s")
+
+    traffic = None
+    tf = ROOT / "profiles" / "decode_traffic.json"
+    if tf.exists():
+        try:
+            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+
+    line = {
+        "metric": "decode-attn HBM GB/s (% of peak) @32K ctx; prefill-attn TFLOPS @8K tokens",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic, seeded N(0,1) (prefill N(0,0.5))",
+        "config": {"workload": "C3 Flash-Decode: 1 query token, 16 query heads / 4 KV heads, "
+                               "head_dim 128, L=32768, KV rotated over 8 buffers (HBM-cold)",
+                   "kv_len": L, "num_heads": HQ, "num_kv_heads": HKV, "head_dim": D,
+                   "kv_buffers": 8, "parallelism": "single-gpu"},
+        "decode_pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+        "prefill": {"workload": "C4 causal GQA prefill, N=8192 tokens, 16/4 heads, D=128",
+                    "us": round(pms * 1e3, 2), "tflops": round(tflops, 2),
+                    "pct_of_fp16_peak": round(100 * tflops / PEAK_FP16_TFLOPS, 2)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic},
+        "roofline_prefill": {"bound": "mfma", "achieved": round(tflops, 2),
+                             "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(tflops / PEAK_FP16_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": (cpu or {}).get("oracle"),
+        "detail": detail,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

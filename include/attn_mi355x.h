@@ -1,0 +1,137 @@
+/*
+ * attn_mi355x.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Drop-in replacement for the attention launch API of MarcVivas/llm-inference
+ * (include/kernels/kernels.hpp).  Each entry point names the reference
+ * declaration it replaces.  All device buffers are caller-owned; no entry
+ * point allocates, frees or copies host<->device, so every launch is safe to
+ * record into a HIP graph.  fp16 buffers are IEEE binary16 (attn_f16_t holds
+ * the bit pattern).  Strides are in elements between consecutive tokens; a
+ * stride of 0 means "packed" (causal_attention.hip.cpp:412-413, :875-876).
+ *
+ * Return value: 0 (hipSuccess) or a hipError_t code.  Shapes the reference
+ * launchers silently ignore (seq_len == 0, kv_len == 0, num_kv_heads == 0,
+ * num_heads % num_kv_heads != 0; causal_attention.hip.cpp:392-399, :860-866,
+ * :945-946; rope.hip.cpp:156) return 0 and launch nothing, leaving every
+ * output untouched.
+ */
+#ifndef ATTN_MI355X_H
+#define ATTN_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t attn_f16_t;
+
+/* Decode workspace sizing unit: callers provide num_heads * ceil(kv_len /
+ * ATTN_KV_CHUNK) partial states (kernels.hpp:103 `#define KV_CHUNK 12`). */
+#define ATTN_KV_CHUNK 12
+
+/* Fused RoPE + KV-cache append.
+ * Replaces launch_rope_and_store_kv (kernels.hpp:62-79; rope.hip.cpp:138-196).
+ * Token t: Q heads rotated in place at q + t*q_stride + h*D; K rotated into
+ * k_cache row (start_pos + t) (K source unchanged) and V copied to v_cache row
+ * (start_pos + t); cache rows are num_kv_heads*head_dim elements apart.
+ * apply_rotation == 0 (NoPE layers): K and V copied, Q untouched.
+ * k_cache == NULL: K rotated in place, V untouched (the launch_rope mode).
+ * V is read with k_stride.  cos/sin tables are [max_seq_len][head_dim/2]. */
+int attn_rope_store_kv(attn_f16_t* q, attn_f16_t* k, const attn_f16_t* v,
+                       attn_f16_t* k_cache, attn_f16_t* v_cache,
+                       const attn_f16_t* cos_table, const attn_f16_t* sin_table,
+                       size_t seq_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
+                       size_t q_stride, size_t k_stride, size_t start_pos,
+                       int apply_rotation, hipStream_t stream);
+
+/* In-place RoPE of Q and K.
+ * Replaces launch_rope (kernels.hpp:47-59; rope.hip.cpp:198-205).  The
+ * reference launches on the null stream; pass NULL for identical behaviour. */
+int attn_rope(attn_f16_t* q, attn_f16_t* k, const attn_f16_t* cos_table,
+              const attn_f16_t* sin_table, size_t seq_len, size_t num_heads,
+              size_t num_kv_heads, size_t head_dim, size_t q_stride, size_t k_stride,
+              size_t start_pos, hipStream_t stream);
+
+/* Re-point a captured RoPE/append node at a new position.
+ * Replaces update_rope_and_store_kv_node (kernels.hpp:81-86;
+ * rope.hip.cpp:208-241). */
+int attn_update_rope_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t start_pos,
+                          int apply_rotation);
+
+/* Causal GQA prefill: query t of head h attends to keys 0..t of KV head
+ * h / (num_heads/num_kv_heads); output packed [seq_len][num_heads][head_dim].
+ * Replaces launch_causal_attention_prefill (kernels.hpp:88-99;
+ * causal_attention.hip.cpp:376-451), which launches on the null stream: pass
+ * NULL for identical behaviour. */
+int attn_prefill(const attn_f16_t* q, const attn_f16_t* k, const attn_f16_t* v,
+                 attn_f16_t* out, size_t seq_len, size_t num_heads, size_t num_kv_heads,
+                 size_t head_dim, size_t q_stride, size_t kv_stride, hipStream_t stream);
+
+/* Flash-Decode of one query token over kv_len cached keys (no mask: all
+ * kv_len keys are visible).  q is read packed [num_heads][head_dim] (q_stride
+ * and start_pos are accepted and unused, as in the reference); out is packed
+ * [num_heads][head_dim].  partial_out/max/sum are caller-owned workspace of at
+ * least num_heads*ceil(kv_len/ATTN_KV_CHUNK) states (partial_out: x head_dim
+ * floats); their contents are private to this library.  Exactly one kernel is
+ * enqueued; when capturing, *attention_node and *merge_node both receive it.
+ * Replaces launch_causal_attention_decode (kernels.hpp:104-123) and
+ * launch_causal_attention_decode_vectorized (kernels.hpp:127-146;
+ * causal_attention.hip.cpp:840-972). */
+int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t* v_cache,
+                attn_f16_t* out, float* partial_out, float* partial_max, float* partial_sum,
+                size_t query_len, size_t kv_len, size_t start_pos, size_t num_heads,
+                size_t num_kv_heads, size_t head_dim, size_t q_stride, size_t kv_stride,
+                hipStream_t stream, hipGraphNode_t* attention_node, hipGraphNode_t* merge_node);
+
+/* Re-point a captured decode node at a new kv_len (grid and split plan are
+ * recomputed).  Replaces update_causal_attention_decode_node
+ * (kernels.hpp:190-194; causal_attention.hip.cpp:975-1001). */
+int attn_update_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len);
+
+/* Companion of attn_update_decode_node for the merge node.  The merge runs
+ * inside the decode kernel, so for nodes returned by attn_decode this is a
+ * no-op that validates the node.  Replaces update_merge_attention_decode_node
+ * (kernels.hpp:148-152; causal_attention.hip.cpp:1003-1026). */
+int attn_update_merge_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len);
+
+/* Workspace states a caller must provide for kv_len keys:
+ * num_heads * ceil(kv_len / ATTN_KV_CHUNK) (model_inference.hpp:192-198). */
+size_t attn_decode_workspace_states(size_t num_heads, size_t kv_len);
+
+/* Host-side RoPE tables, fp16 [max_seq_len][head_dim/2]: inv_freq[i] =
+ * 1/powf(theta, 2i/D), angle = float(pos)*inv_freq[i], cos/sin in fp32 then
+ * RNE to fp16.  Same tables as rope_cache.hpp:48-76 (create_rope_cache minus
+ * the upload).  Pure host code. */
+int attn_rope_tables(attn_f16_t* cos_out, attn_f16_t* sin_out, size_t max_seq_len,
+                     size_t head_dim, float rope_theta);
+
+/* Introspection for tests and benchmarks: the decode plan chosen for a shape
+ * on the current device.  out[0] = path (0 generic, 1 MFMA 4-wave, 2 MFMA
+ * 8-wave), out[1] = splits per KV head, out[2] = keys per split,
+ * out[3] = threads per workgroup. */
+int attn_decode_plan(size_t kv_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
+                     size_t kv_stride, const void* q, const void* k_cache,
+                     const void* v_cache, uint32_t out[4]);
+
+/* Prefill path chosen for a shape: 0 generic, 1 MFMA. */
+int attn_prefill_plan(const void* q, const void* k, const void* v, const void* out,
+                      size_t num_heads, size_t num_kv_heads, size_t head_dim, size_t q_stride,
+                      size_t kv_stride);
+
+/* Process-wide switches for tests and benchmarks (not needed in production):
+ * "decode_force_generic", "decode_splits" (0 = automatic), "decode_waves"
+ * (4 or 8; 0 = automatic), "prefill_force_generic".  Returns 0 or -1 for an
+ * unknown name. */
+int attn_set_option(const char* name, long value);
+
+/* Library build identification (static string). */
+const char* attn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATTN_MI355X_H */

@@ -1,0 +1,350 @@
+// C-ABI entry points of libattn_mi355x.so (declared in include/attn_mi355x.h).
+// Argument checking and no-op rules mirror the reference launchers; kernels
+// are chosen per shape (MFMA/vector paths for the SmolLM3 shapes, generic
+// kernels for everything else).  Nothing here allocates device memory, so
+// every launch can be captured into a HIP graph.
+#include "attn_internal.hpp"
+#include "../../include/attn_mi355x.h"
+
+#include <atomic>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+
+namespace attn {
+
+namespace {
+
+std::atomic<long> g_options[kOptCount];
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+
+hipError_t captured_node(hipStream_t stream, hipGraphNode_t* out) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    const hipGraphNode_t* deps = nullptr;
+    size_t count = 0;
+    hipError_t e = hipStreamGetCaptureInfo_v2(stream, &status, nullptr, nullptr, &deps, &count);
+    if (e != hipSuccess) return e;
+    // gpu_utils.hpp:45-59: exactly one capture dependency is expected
+    if (status != hipStreamCaptureStatusActive || count != 1 || deps == nullptr)
+        return hipErrorIllegalState;
+    *out = deps[0];
+    return hipSuccess;
+}
+
+bool fits_u32(size_t v) { return v <= 0xffffffffull; }
+
+float scale_log2_for(size_t head_dim) {
+    return (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+}
+
+}  // namespace
+
+long get_option(int which) {
+    if (which < 0 || which >= kOptCount) return 0;
+    return g_options[which].load(std::memory_order_relaxed);
+}
+
+int device_cu_count(int device) {
+    if (device < 0 || device >= kMaxDevices) return 256;
+    int v = g_cu_count[device].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        cus <= 0)
+        cus = 256;
+    g_cu_count[device].store(cus, std::memory_order_relaxed);
+    return cus;
+}
+
+}  // namespace attn
+
+using namespace attn;
+
+extern "C" {
+
+const char* attn_version(void) { return "attn_mi355x 0.1 gfx950"; }
+
+int attn_set_option(const char* name, long value) {
+    if (!name) return -1;
+    int which = -1;
+    if (!std::strcmp(name, "decode_force_generic")) which = kOptDecodeForceGeneric;
+    else if (!std::strcmp(name, "decode_splits")) which = kOptDecodeSplits;
+    else if (!std::strcmp(name, "prefill_force_generic")) which = kOptPrefillForceGeneric;
+    else if (!std::strcmp(name, "decode_waves")) which = kOptDecodeWaves;
+    if (which < 0) return -1;
+    g_options[which].store(value, std::memory_order_relaxed);
+    return 0;
+}
+
+size_t attn_decode_workspace_states(size_t num_heads, size_t kv_len) {
+    return num_heads * ((kv_len + ATTN_KV_CHUNK - 1) / ATTN_KV_CHUNK);
+}
+
+int attn_rope_tables(attn_f16_t* cos_out, attn_f16_t* sin_out, size_t max_seq_len,
+                     size_t head_dim, float rope_theta) {
+    if (!cos_out || !sin_out || head_dim < 2) return (int)hipErrorInvalidValue;
+    const size_t half = head_dim / 2;
+    for (size_t i = 0; i < half; ++i) {
+        const float exponent = (float)(2 * i) / (float)head_dim;
+        const float inv_freq = 1.0f / std::pow(rope_theta, exponent);
+        for (size_t pos = 0; pos < max_seq_len; ++pos) {
+            const float angle = (float)pos * inv_freq;
+            const _Float16 c = (_Float16)std::cos(angle);
+            const _Float16 s = (_Float16)std::sin(angle);
+            std::memcpy(&cos_out[pos * half + i], &c, 2);
+            std::memcpy(&sin_out[pos * half + i], &s, 2);
+        }
+    }
+    return 0;
+}
+
+int attn_rope_store_kv(attn_f16_t* q, attn_f16_t* k, const attn_f16_t* v,
+                       attn_f16_t* k_cache, attn_f16_t* v_cache,
+                       const attn_f16_t* cos_table, const attn_f16_t* sin_table,
+                       size_t seq_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
+                       size_t q_stride, size_t k_stride, size_t start_pos,
+                       int apply_rotation, hipStream_t stream) {
+    if (seq_len == 0) return 0;  // rope.hip.cpp:156
+    if (head_dim == 0 || (head_dim & 1u)) return (int)hipErrorInvalidValue;
+    if (!apply_rotation && k_cache == nullptr) return (int)hipErrorInvalidValue;
+    if (k_cache && (!v_cache || !v)) return (int)hipErrorInvalidValue;
+    if (!fits_u32(seq_len) || !fits_u32(num_heads) || !fits_u32(num_kv_heads) ||
+        !fits_u32(head_dim) || !fits_u32(start_pos + seq_len))
+        return (int)hipErrorInvalidValue;
+    RopeArgs a{};
+    a.q = reinterpret_cast<f16*>(q);
+    a.k = reinterpret_cast<f16*>(k);
+    a.v = reinterpret_cast<const f16*>(v);
+    a.kc = reinterpret_cast<f16*>(k_cache);
+    a.vc = reinterpret_cast<f16*>(v_cache);
+    a.cos_t = reinterpret_cast<const f16*>(cos_table);
+    a.sin_t = reinterpret_cast<const f16*>(sin_table);
+    a.q_stride = q_stride ? q_stride : num_heads * head_dim;
+    a.k_stride = k_stride ? k_stride : num_kv_heads * head_dim;
+    a.seq_len = (uint32_t)seq_len;
+    a.num_heads = (uint32_t)num_heads;
+    a.num_kv_heads = (uint32_t)num_kv_heads;
+    a.head_dim = (uint32_t)head_dim;
+    a.start_pos = (uint32_t)start_pos;
+    a.apply = apply_rotation ? 1u : 0u;
+    a.lanes_per_head = (uint32_t)(head_dim / 16);
+    const bool vec = rope_vector_ok(a);
+    return (int)launch_rope_kernel(a, vec, stream);
+}
+
+int attn_rope(attn_f16_t* q, attn_f16_t* k, const attn_f16_t* cos_table,
+              const attn_f16_t* sin_table, size_t seq_len, size_t num_heads,
+              size_t num_kv_heads, size_t head_dim, size_t q_stride, size_t k_stride,
+              size_t start_pos, hipStream_t stream) {
+    return attn_rope_store_kv(q, k, nullptr, nullptr, nullptr, cos_table, sin_table, seq_len,
+                              num_heads, num_kv_heads, head_dim, q_stride, k_stride, start_pos,
+                              1, stream);
+}
+
+int attn_update_rope_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t start_pos,
+                          int apply_rotation) {
+    hipKernelNodeParams params{};
+    hipError_t e = hipGraphKernelNodeGetParams(node, &params);
+    if (e != hipSuccess) return (int)e;
+    if (params.func != rope_kernel_symbol(true) && params.func != rope_kernel_symbol(false))
+        return (int)hipErrorInvalidValue;
+    RopeArgs a = *reinterpret_cast<const RopeArgs*>(params.kernelParams[0]);
+    if (!fits_u32(start_pos + a.seq_len)) return (int)hipErrorInvalidValue;
+    if (!apply_rotation && a.kc == nullptr) return (int)hipErrorInvalidValue;
+    a.start_pos = (uint32_t)start_pos;
+    a.apply = apply_rotation ? 1u : 0u;
+    void* args[1] = {&a};
+    params.kernelParams = args;
+    params.extra = nullptr;
+    return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
+}
+
+int attn_prefill_plan(const void* q, const void* k, const void* v, const void* out,
+                      size_t num_heads, size_t num_kv_heads, size_t head_dim, size_t q_stride,
+                      size_t kv_stride) {
+    if (num_kv_heads == 0 || num_heads % num_kv_heads != 0) return -1;
+    PrefillArgs a{};
+    a.q = reinterpret_cast<const f16*>(q);
+    a.k = reinterpret_cast<const f16*>(k);
+    a.v = reinterpret_cast<const f16*>(v);
+    a.out = reinterpret_cast<f16*>(const_cast<void*>(out));
+    a.q_stride = q_stride ? q_stride : num_heads * head_dim;
+    a.kv_stride = kv_stride ? kv_stride : num_kv_heads * head_dim;
+    a.num_heads = (uint32_t)num_heads;
+    a.num_kv_heads = (uint32_t)num_kv_heads;
+    a.group = (uint32_t)(num_heads / num_kv_heads);
+    a.head_dim = (uint32_t)head_dim;
+    return plan_prefill(a);
+}
+
+int attn_prefill(const attn_f16_t* q, const attn_f16_t* k, const attn_f16_t* v,
+                 attn_f16_t* out, size_t seq_len, size_t num_heads, size_t num_kv_heads,
+                 size_t head_dim, size_t q_stride, size_t kv_stride, hipStream_t stream) {
+    // causal_attention.hip.cpp:392-399
+    if (seq_len == 0 || num_kv_heads == 0) return 0;
+    if (num_heads % num_kv_heads != 0) return 0;
+    if (head_dim == 0) return 0;
+    if (!fits_u32(seq_len) || !fits_u32(num_heads) || !fits_u32(head_dim))
+        return (int)hipErrorInvalidValue;
+    PrefillArgs a{};
+    a.q = reinterpret_cast<const f16*>(q);
+    a.k = reinterpret_cast<const f16*>(k);
+    a.v = reinterpret_cast<const f16*>(v);
+    a.out = reinterpret_cast<f16*>(out);
+    a.q_stride = q_stride ? q_stride : num_heads * head_dim;
+    a.kv_stride = kv_stride ? kv_stride : num_kv_heads * head_dim;
+    a.seq_len = (uint32_t)seq_len;
+    a.num_heads = (uint32_t)num_heads;
+    a.num_kv_heads = (uint32_t)num_kv_heads;
+    a.group = (uint32_t)(num_heads / num_kv_heads);
+    a.head_dim = (uint32_t)head_dim;
+    a.q_tiles = (uint32_t)((seq_len + 63) / 64);
+    a.scale_log2 = scale_log2_for(head_dim);
+    const int path = plan_prefill(a);
+    if (path == 1) return (int)launch_prefill_kernel(a, path, stream);
+    GenericAttnArgs g{};
+    g.q = a.q;
+    g.k = a.k;
+    g.v = a.v;
+    g.out = a.out;
+    g.q_stride = a.q_stride;
+    g.kv_stride = a.kv_stride;
+    g.nq = a.seq_len;
+    g.kv_len = a.seq_len;
+    g.num_heads = a.num_heads;
+    g.group = a.group;
+    g.head_dim = a.head_dim;
+    g.causal = 1;
+    g.scale_log2 = a.scale_log2;
+    return (int)launch_generic_attention(g, stream);
+}
+
+int attn_decode_plan(size_t kv_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
+                     size_t kv_stride, const void* q, const void* k_cache,
+                     const void* v_cache, uint32_t out[4]) {
+    if (!out || num_kv_heads == 0 || num_heads % num_kv_heads != 0 || kv_len == 0) return -1;
+    int device = 0;
+    (void)hipGetDevice(&device);
+    const size_t kvs = kv_stride ? kv_stride : num_kv_heads * head_dim;
+    const DecodePlan p = plan_decode((uint32_t)kv_len, (uint32_t)num_heads,
+                                     (uint32_t)num_kv_heads, (uint32_t)head_dim, kvs, q,
+                                     k_cache, v_cache, device);
+    out[0] = (uint32_t)p.path;
+    out[1] = p.nsplit;
+    out[2] = p.chunk;
+    out[3] = p.block;
+    return 0;
+}
+
+int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t* v_cache,
+                attn_f16_t* out, float* partial_out, float* partial_max, float* partial_sum,
+                size_t query_len, size_t kv_len, size_t start_pos, size_t num_heads,
+                size_t num_kv_heads, size_t head_dim, size_t q_stride, size_t kv_stride,
+                hipStream_t stream, hipGraphNode_t* attention_node, hipGraphNode_t* merge_node) {
+    (void)start_pos;  // all kv_len keys are visible (causal_attention.hip.cpp:943)
+    (void)q_stride;   // q is read packed [num_heads][head_dim] (:944)
+    // causal_attention.hip.cpp:860-866, :945-946
+    if (query_len == 0 || kv_len == 0 || num_kv_heads == 0 || head_dim == 0) return 0;
+    if (num_heads % num_kv_heads != 0) return 0;
+    if (!fits_u32(kv_len) || !fits_u32(num_heads) || !fits_u32(head_dim))
+        return (int)hipErrorInvalidValue;
+    const size_t kvs = kv_stride ? kv_stride : num_kv_heads * head_dim;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return (int)e;
+    const DecodePlan p = plan_decode((uint32_t)kv_len, (uint32_t)num_heads,
+                                     (uint32_t)num_kv_heads, (uint32_t)head_dim, kvs, q,
+                                     k_cache, v_cache, device);
+    if (p.path == 0) {
+        GenericAttnArgs g{};
+        g.q = reinterpret_cast<const f16*>(q);
+        g.k = reinterpret_cast<const f16*>(k_cache);
+        g.v = reinterpret_cast<const f16*>(v_cache);
+        g.out = reinterpret_cast<f16*>(out);
+        g.q_stride = num_heads * head_dim;
+        g.kv_stride = kvs;
+        g.nq = 1;
+        g.kv_len = (uint32_t)kv_len;
+        g.num_heads = (uint32_t)num_heads;
+        g.group = (uint32_t)(num_heads / num_kv_heads);
+        g.head_dim = (uint32_t)head_dim;
+        g.causal = 0;
+        g.scale_log2 = scale_log2_for(head_dim);
+        e = launch_generic_attention(g, stream);
+    } else {
+        if (!partial_out || !partial_max || !partial_sum) return (int)hipErrorInvalidValue;
+        DecodeArgs a{};
+        a.q = reinterpret_cast<const f16*>(q);
+        a.k = reinterpret_cast<const f16*>(k_cache);
+        a.v = reinterpret_cast<const f16*>(v_cache);
+        a.out = reinterpret_cast<f16*>(out);
+        a.part_out = partial_out;
+        a.part_max = partial_max;
+        a.part_sum = partial_sum;
+        a.kv_stride = kvs;
+        a.kv_len = (uint32_t)kv_len;
+        a.num_heads = (uint32_t)num_heads;
+        a.num_kv_heads = (uint32_t)num_kv_heads;
+        a.group = (uint32_t)(num_heads / num_kv_heads);
+        a.head_dim = (uint32_t)head_dim;
+        a.scale_log2 = scale_log2_for(head_dim);
+        replan_decode(a, p.path, device);
+        e = launch_decode_kernel(a, p, stream);
+    }
+    if (e != hipSuccess) return (int)e;
+    if (attention_node || merge_node) {
+        hipGraphNode_t node = nullptr;
+        e = captured_node(stream, &node);
+        if (e != hipSuccess) return (int)e;
+        if (attention_node) *attention_node = node;
+        if (merge_node) *merge_node = node;
+    }
+    return 0;
+}
+
+int attn_update_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len) {
+    if (kv_len == 0 || !fits_u32(kv_len)) return (int)hipErrorInvalidValue;
+    hipKernelNodeParams params{};
+    hipError_t e = hipGraphKernelNodeGetParams(node, &params);
+    if (e != hipSuccess) return (int)e;
+    if (params.func == generic_attention_symbol()) {
+        GenericAttnArgs g = *reinterpret_cast<const GenericAttnArgs*>(params.kernelParams[0]);
+        if (g.causal) return (int)hipErrorInvalidValue;  // not a decode node
+        g.kv_len = (uint32_t)kv_len;
+        void* args[1] = {&g};
+        params.kernelParams = args;
+        params.extra = nullptr;
+        return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
+    }
+    int path = 0;
+    if (params.func == decode_kernel_symbol(1)) path = 1;
+    else if (params.func == decode_kernel_symbol(2)) path = 2;
+    else return (int)hipErrorInvalidValue;
+    DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(params.kernelParams[0]);
+    int device = 0;
+    e = hipGetDevice(&device);
+    if (e != hipSuccess) return (int)e;
+    a.kv_len = (uint32_t)kv_len;
+    replan_decode(a, path, device);
+    void* args[1] = {&a};
+    params.kernelParams = args;
+    params.extra = nullptr;
+    params.gridDim.x = a.nsplit;
+    return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
+}
+
+int attn_update_merge_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len) {
+    (void)graph_exec;
+    (void)kv_len;
+    hipKernelNodeParams params{};
+    hipError_t e = hipGraphKernelNodeGetParams(node, &params);
+    if (e != hipSuccess) return (int)e;
+    if (params.func == generic_attention_symbol() || params.func == decode_kernel_symbol(1) ||
+        params.func == decode_kernel_symbol(2))
+        return 0;
+    return (int)hipErrorInvalidValue;
+}
+
+}  // extern "C"

@@ -1,0 +1,42 @@
+// Shared device/host helpers for the gfx950 (CDNA4, wave64) attention path.
+// All kernels in this library are written for wave64 and gfx950's MFMA
+// instruction set; nothing here targets another architecture.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace attn {
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+
+// 16-byte global load/store of eight fp16 values (pointer must be 16B aligned).
+__device__ __forceinline__ f16x8 ld16(const f16* p) {
+    return *reinterpret_cast<const f16x8*>(p);
+}
+__device__ __forceinline__ void st16(f16* p, f16x8 v) {
+    *reinterpret_cast<f16x8*>(p) = v;
+}
+
+// Cross-lane exchange inside a wave64 (ds_bpermute based).
+__device__ __forceinline__ float xor_lane(float v, int mask) {
+    return __shfl_xor(v, mask, kWave);
+}
+
+// 2^x on the hardware transcendental unit (v_exp_f32).  Softmax is computed
+// in the log2 domain: scores are pre-multiplied by log2(e)/sqrt(D).
+__device__ __forceinline__ float fast_exp2(float x) {
+    return __builtin_amdgcn_exp2f(x);
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace attn

@@ -1,0 +1,129 @@
+// Internal interface between the kernel translation units and the C-ABI layer.
+// Every kernel takes ONE argument struct by value, so a captured graph node can
+// be re-parameterised by copying the struct out of hipKernelNodeParams,
+// editing fields and writing it back (the update_*_node entry points).
+#pragma once
+
+#include "attn_common.hpp"
+
+namespace attn {
+
+// ------------------------------------------------------------- RoPE + append
+struct RopeArgs {
+    f16* q;             // [seq, q_stride], Q heads rotated in place
+    f16* k;             // [seq, k_stride] K source (rotated in place when kc == nullptr)
+    const f16* v;       // [seq, k_stride] V source
+    f16* kc;            // K cache rows [S][Hkv*D] or nullptr
+    f16* vc;            // V cache rows [S][Hkv*D]
+    const f16* cos_t;   // [S][D/2]
+    const f16* sin_t;   // [S][D/2]
+    uint64_t q_stride;  // elements between Q tokens
+    uint64_t k_stride;  // elements between K/V source tokens
+    uint32_t seq_len;
+    uint32_t num_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t start_pos;      // cache row / table row of token 0 (patched per decode step)
+    uint32_t apply;          // 1: rotate Q and K; 0: NoPE, copy K and V only (patched)
+    uint32_t lanes_per_head; // vector path: D/16 lanes per head (each lane = 8 pairs)
+    uint32_t pad_;
+};
+
+hipError_t launch_rope_kernel(const RopeArgs& a, bool vector_path, hipStream_t stream);
+bool rope_vector_ok(const RopeArgs& a);
+const void* rope_kernel_symbol(bool vector_path);
+
+// ------------------------------------------------------------- Flash-Decode
+struct DecodeArgs {
+    const f16* q;        // [Hq][D] packed
+    const f16* k;        // cache rows, kv_stride elements apart
+    const f16* v;
+    f16* out;            // [Hq][D] packed
+    float* part_out;     // [Hq][nsplit][D]   (workspace)
+    float* part_max;     // [Hq][nsplit]      (workspace, log2 domain)
+    float* part_sum;     // [Hq][nsplit]      (workspace)
+    unsigned long long* counters;  // [Hkv] arrival counters inside part_sum's tail
+    uint64_t kv_stride;
+    uint32_t kv_len;     // patched per decode step
+    uint32_t num_heads;
+    uint32_t num_kv_heads;
+    uint32_t group;      // Hq / Hkv
+    uint32_t head_dim;
+    uint32_t nsplit;     // context splits per KV head (patched)
+    uint32_t chunk;      // keys per split (patched)
+    uint32_t epoch;      // arrival-counter generation (patched)
+    float scale_log2;    // log2(e) / sqrt(D)
+    uint32_t pad_;
+};
+
+struct DecodePlan {
+    int path;          // 0 = generic (any D, any stride), 1 = MFMA wave64 path (D = 128)
+    uint32_t nsplit;
+    uint32_t chunk;
+    uint32_t block;    // threads per workgroup
+};
+
+DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_heads,
+                       uint32_t head_dim, uint64_t kv_stride, const void* q, const void* k,
+                       const void* v, int device);
+// Recompute split/chunk/counter fields of an existing argument struct for a
+// new kv_len (same path).  Used by launch and by the graph-node updater.
+void replan_decode(DecodeArgs& a, int path, int device);
+hipError_t launch_decode_kernel(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream);
+const void* decode_kernel_symbol(int path);
+
+// ------------------------------------------------------------- prefill
+struct PrefillArgs {
+    const f16* q;       // [N] rows, q_stride elements apart, Hq heads of D
+    const f16* k;       // [N] rows, kv_stride apart, Hkv heads of D
+    const f16* v;
+    f16* out;           // packed [N][Hq][D]
+    uint64_t q_stride;
+    uint64_t kv_stride;
+    uint32_t seq_len;
+    uint32_t num_heads;
+    uint32_t num_kv_heads;
+    uint32_t group;
+    uint32_t head_dim;
+    uint32_t q_tiles;   // MFMA path: number of 64-token query tiles
+    float scale_log2;
+    uint32_t pad_;
+};
+
+int plan_prefill(const PrefillArgs& a);  // 0 generic, 1 MFMA
+hipError_t launch_prefill_kernel(const PrefillArgs& a, int path, hipStream_t stream);
+
+// generic attention (one workgroup per query row and head); also the decode
+// fallback for head_dim != 128 or unaligned strides
+struct GenericAttnArgs {
+    const f16* q;
+    const f16* k;
+    const f16* v;
+    f16* out;
+    uint64_t q_stride;
+    uint64_t kv_stride;
+    uint32_t nq;        // query rows
+    uint32_t kv_len;    // keys visible to every row (patched for decode)
+    uint32_t num_heads;
+    uint32_t group;
+    uint32_t head_dim;
+    uint32_t causal;    // 1: row t sees keys <= t (start position 0)
+    float scale_log2;
+    uint32_t pad_;
+};
+hipError_t launch_generic_attention(const GenericAttnArgs& a, hipStream_t stream);
+const void* generic_attention_symbol();
+
+// option switches for tests/benchmarks (process-wide)
+enum Option {
+    kOptDecodeForceGeneric = 0,
+    kOptDecodeSplits = 1,        // 0 = automatic
+    kOptPrefillForceGeneric = 2,
+    kOptDecodeWaves = 3,         // 0 = automatic
+    kOptCount = 8
+};
+long get_option(int which);
+
+int device_cu_count(int device);
+
+}  // namespace attn

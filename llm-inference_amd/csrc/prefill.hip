@@ -1,0 +1,274 @@
+// Causal grouped-query prefill attention for gfx950 on fp16 MFMA.
+//
+// Reference semantics: causal_attention.hip.cpp:271-374 with the launcher
+// :376-451 -- query t of head h attends to keys 0..t of KV head h/(Hq/Hkv),
+// scores q.k/sqrt(D), softmax in fp32, output packed [N][Hq][D] fp16; start
+// position 0 and kv_len = N (:388-390).
+//
+// MFMA path (D = 128, Hq/Hkv a multiple of 4, 16-byte aligned rows):
+//  * workgroup = 4 waves = 4 query heads sharing one KV head, 64 query tokens.
+//    Every wave owns 64 queries of its head (two 32-column MFMA tiles) so each
+//    K/V operand fetched from LDS feeds two MFMAs.
+//  * K and V of a 64-key tile are staged in LDS once per workgroup and shared
+//    by the 4 heads (the reference re-reads them per head).  V is stored
+//    transposed (V^T[dim][key]) with the keys of every 16-key MFMA step in the
+//    order the S^T accumulator produces them, so P never leaves registers.
+//  * S^T = K . Q^T with v_mfma_f32_32x32x16_f16: keys are MFMA rows, queries
+//    columns, so each lane holds one query's scores and the online softmax
+//    (running max, running sum, rescale) is per lane plus one xor-32 exchange.
+//  * O^T = V^T . P^T on the same MFMA; O^T stays in 64 accumulator registers.
+//  * Causal tile skipping: query tile i visits key tiles 0..i only; the
+//    diagonal tile is masked.  Tiles are handed out longest-first and the
+//    four head groups of one KV head are kept on the same pair of XCDs so the
+//    KV head's K/V stays in one L2.
+//  * K/V tile j+1 is prefetched into registers while tile j is computed; two
+//    LDS buffers, one barrier per tile.
+#include "attn_internal.hpp"
+
+namespace attn {
+
+namespace {
+
+constexpr int kD = 128;
+constexpr int kBM = 64;        // query tokens per workgroup (per wave)
+constexpr int kBN = 64;        // keys per tile
+constexpr int kKP = kD + 8;    // K tile row pitch (halves): conflict-free 16 B reads
+constexpr int kVP = kBN + 8;   // V^T tile row pitch (halves)
+
+__device__ __forceinline__ f16x8 lds16(const f16* p) {
+    return *reinterpret_cast<const f16x8*>(p);
+}
+
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// blockIdx -> (head quad, query tile), longest tiles first, head quads pinned
+// to XCD subsets (workgroups are dispatched round-robin over the 8 XCDs).
+__device__ __forceinline__ bool map_block(uint32_t bid, uint32_t quads, uint32_t q_tiles,
+                                          uint32_t& quad, uint32_t& tile) {
+    if (quads <= 8 && (8 % quads) == 0) {
+        const uint32_t xcd = bid & 7u;
+        const uint32_t j = bid >> 3;
+        const uint32_t per = 8u / quads;
+        quad = xcd % quads;
+        const uint32_t rank = j * per + xcd / quads;
+        if (rank >= q_tiles) return false;
+        tile = q_tiles - 1u - rank;
+        return true;
+    }
+    const uint32_t rank = bid / quads;
+    quad = bid - rank * quads;
+    if (rank >= q_tiles) return false;
+    tile = q_tiles - 1u - rank;
+    return true;
+}
+
+__global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) f16 kt[2][kBN * kKP];
+    __shared__ __attribute__((aligned(16))) f16 vt[2][kD * kVP];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n = lane & 31;   // MFMA column (query) / A-operand row
+    const int hh = lane >> 5;  // MFMA k-half / output row half
+
+    const uint32_t quads = a.num_heads / 4u;
+    uint32_t quad, tile;
+    if (!map_block(blockIdx.x, quads, a.q_tiles, quad, tile)) return;
+    const uint32_t head = 4u * quad + (uint32_t)wave;
+    const uint32_t g = (4u * quad) / a.group;
+    const uint32_t N = a.seq_len;
+    const uint32_t q0 = tile * kBM;
+
+    // Q^T B operands: lane (hh, n) of column tile nt holds
+    // Q[q0 + 32nt + n][head][16s + 8hh .. +7] for k-step s.
+    f16x8 qb[2][8];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const uint32_t row = q0 + 32u * nt + n;
+        if (row < N) {
+            const f16* p = a.q + (uint64_t)row * a.q_stride + (uint64_t)head * kD + 8 * hh;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) qb[nt][s] = ld16(p + 16 * s);
+        } else {
+#pragma unroll
+            for (int s = 0; s < 8; ++s) qb[nt][s] = f16x8{};
+        }
+    }
+
+    f32x16 o[2][4];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[nt][dt] = f32x16{};
+    float m_run[2] = {-INFINITY, -INFINITY};
+    float l_run[2] = {0.f, 0.f};
+
+    // global -> register staging of one 64-key tile
+    const f16* kbase = a.k + (uint64_t)g * kD;
+    const f16* vbase = a.v + (uint64_t)g * kD;
+    const uint32_t kq = tid & 15;   // V: key quad (keys 4kq..4kq+3)
+    const uint32_t dg = tid >> 4;   // V: dims 8dg..8dg+7
+    f16x8 kr[4], vr[4];
+    auto gload = [&](uint32_t kv0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t e = (uint32_t)i * 256u + tid;
+            const uint32_t key = kv0 + (e >> 4);
+            kr[i] = key < N ? ld16(kbase + (uint64_t)key * a.kv_stride + 8u * (e & 15u)) : f16x8{};
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t key = kv0 + 4u * kq + r;
+            vr[r] = key < N ? ld16(vbase + (uint64_t)key * a.kv_stride + 8u * dg) : f16x8{};
+        }
+    };
+    // key quad kq = 4ks + 2b + h lands in V^T slots ks*16 + h*8 + 4b .. +3,
+    // the order in which S^T tile ks/2 presents keys to PV k-step ks.
+    const uint32_t vslot = (kq >> 2) * 16u + (kq & 1u) * 8u + ((kq >> 1) & 1u) * 4u;
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t e = (uint32_t)i * 256u + tid;
+            *reinterpret_cast<f16x8*>(&kt[buf][(e >> 4) * kKP + 8u * (e & 15u)]) = kr[i];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            f16x4 w;
+            w[0] = vr[0][j];
+            w[1] = vr[1][j];
+            w[2] = vr[2][j];
+            w[3] = vr[3][j];
+            *reinterpret_cast<f16x4*>(&vt[buf][(8u * dg + j) * kVP + vslot]) = w;
+        }
+    };
+
+    const uint32_t n_tiles = tile + 1u;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+
+    for (uint32_t j = 0; j < n_tiles; ++j) {
+        const int buf = (int)(j & 1u);
+        if (j + 1 < n_tiles) gload((j + 1) * kBN);
+
+        // ---- S^T[key][query] = K . Q^T
+        f32x16 s[2][2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) s[nt][mt] = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const f16x8 ka = lds16(&kt[buf][(32 * mt + n) * kKP + 16 * ks + 8 * hh]);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) s[nt][mt] = mfma32(ka, qb[nt][ks], s[nt][mt]);
+            }
+        }
+
+        // ---- online softmax (log2 domain), per lane = per query
+        const bool diag = (j == tile);
+        f16x8 pb[2][4];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const uint32_t query = q0 + 32u * nt + n;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    float x = s[nt][mt][i];
+                    if (diag) {
+                        const uint32_t key = j * kBN + 32u * mt + 8u * (i >> 2) + 4u * hh + (i & 3);
+                        if (key > query || key >= N) x = -INFINITY;
+                    }
+                    s[nt][mt][i] = x;
+                    mx = fmaxf(mx, x);
+                }
+            mx = fmaxf(mx, xor_lane(mx, 32));
+            const float m_new = fmaxf(m_run[nt], mx * a.scale_log2);
+            const float alpha = fast_exp2(m_run[nt] - m_new);
+            float psum = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    const float x = s[nt][ks >> 1][8 * (ks & 1) + r];
+                    const f16 p = (f16)fast_exp2(__builtin_fmaf(x, a.scale_log2, -m_new));
+                    pb[nt][ks][r] = p;
+                    psum += (float)p;
+                }
+            l_run[nt] = l_run[nt] * alpha + psum;
+            m_run[nt] = m_new;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[nt][dt] *= alpha;
+        }
+
+        // ---- O^T[dim][query] += V^T . P^T
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const f16x8 va = lds16(&vt[buf][(32 * dt + n) * kVP + 16 * ks + 8 * hh]);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) o[nt][dt] = mfma32(va, pb[nt][ks], o[nt][dt]);
+            }
+        }
+
+        if (j + 1 < n_tiles) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue: O = O^T / l, packed [N][Hq][D]
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const float l = l_run[nt] + xor_lane(l_run[nt], 32);
+        const float inv = 1.f / l;
+        const uint32_t query = q0 + 32u * nt + n;
+        if (query >= N) continue;
+        f16* orow = a.out + ((uint64_t)query * a.num_heads + head) * kD;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                f16x4 w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = (f16)(o[nt][dt][4 * i4 + e] * inv);
+                *reinterpret_cast<f16x4*>(orow + 32 * dt + 8 * i4 + 4 * hh) = w;
+            }
+    }
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+int plan_prefill(const PrefillArgs& a) {
+    if (get_option(kOptPrefillForceGeneric)) return 0;
+    if (a.head_dim != kD) return 0;
+    if (a.group == 0 || a.group % 4 != 0 || a.num_heads % 4 != 0) return 0;
+    if (a.q_stride % 8 != 0 || a.kv_stride % 8 != 0) return 0;
+    if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v) || !aligned16(a.out)) return 0;
+    return 1;
+}
+
+hipError_t launch_prefill_kernel(const PrefillArgs& a, int path, hipStream_t stream) {
+    if (path != 1) return hipErrorInvalidValue;
+    const uint32_t quads = a.num_heads / 4u;
+    uint64_t blocks;
+    if (quads <= 8 && (8 % quads) == 0) {
+        const uint32_t per = 8u / quads;
+        blocks = 8ull * ((a.q_tiles + per - 1) / per);
+    } else {
+        blocks = (uint64_t)a.q_tiles * quads;
+    }
+    if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(prefill_d128, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace attn

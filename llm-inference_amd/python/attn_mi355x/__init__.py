@@ -1,0 +1,217 @@
+"""Python harness for libattn_mi355x.so (the MI355X attention hot path).
+
+This module is a thin ctypes binding of the C ABI declared in
+include/attn_mi355x.h.  It mirrors the reference's launch API
+(include/kernels/kernels.hpp of MarcVivas/llm-inference): same argument
+names, meanings and no-op rules.  Device memory and streams come from
+PyTorch (plumbing only); every computation runs in the HIP kernels of the
+library.  There is no CPU fallback: if the library is missing, loading fails
+loudly.
+
+torch is imported before the library is loaded so that both bind the same HIP
+runtime (both are linked against SONAME libamdhip64.so.7).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import pathlib
+from typing import Optional
+
+import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
+
+PKG_ROOT = pathlib.Path(__file__).resolve().parents[2]
+LIB_PATH = PKG_ROOT / "lib" / "libattn_mi355x.so"
+KV_CHUNK = 12  # kernels.hpp:103
+
+_lib = None
+
+_c = ctypes
+_vp = _c.c_void_p
+_sz = _c.c_size_t
+
+
+class AttnError(RuntimeError):
+    pass
+
+
+def _declare(lib):
+    sig = {
+        "attn_rope_store_kv": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz,
+                                          _sz, _sz, _sz, _c.c_int, _vp]),
+        "attn_rope": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
+        "attn_update_rope_node": (_c.c_int, [_vp, _vp, _sz, _c.c_int]),
+        "attn_prefill": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp]),
+        "attn_decode": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz,
+                                   _sz, _sz, _sz, _vp, _vp, _vp]),
+        "attn_update_decode_node": (_c.c_int, [_vp, _vp, _sz]),
+        "attn_update_merge_node": (_c.c_int, [_vp, _vp, _sz]),
+        "attn_decode_workspace_states": (_sz, [_sz, _sz]),
+        "attn_rope_tables": (_c.c_int, [_vp, _vp, _sz, _sz, _c.c_float]),
+        "attn_decode_plan": (_c.c_int, [_sz, _sz, _sz, _sz, _sz, _vp, _vp, _vp,
+                                        _c.POINTER(_c.c_uint32)]),
+        "attn_prefill_plan": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz]),
+        "attn_set_option": (_c.c_int, [_c.c_char_p, _c.c_long]),
+        "attn_version": (_c.c_char_p, []),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def lib():
+    """Load (once) and return the ctypes handle of libattn_mi355x.so."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise AttnError(f"{LIB_PATH} is not built: run `python -c 'import __graft_entry__ as g; g.build()'`")
+        _lib = _declare(ctypes.CDLL(str(LIB_PATH)))
+    return _lib
+
+
+def exported_symbols():
+    """Names declared in include/attn_mi355x.h."""
+    return ["attn_rope_store_kv", "attn_rope", "attn_update_rope_node", "attn_prefill",
+            "attn_decode", "attn_update_decode_node", "attn_update_merge_node",
+            "attn_decode_workspace_states", "attn_rope_tables", "attn_decode_plan",
+            "attn_prefill_plan", "attn_set_option", "attn_version"]
+
+
+def _ptr(x) -> Optional[int]:
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _check(rc: int, what: str):
+    if rc != 0:
+        raise AttnError(f"{what} failed with hipError {rc}")
+
+
+def set_option(name: str, value: int):
+    if lib().attn_set_option(name.encode(), int(value)) != 0:
+        raise AttnError(f"unknown option {name}")
+
+
+def decode_workspace_states(num_heads: int, kv_len: int) -> int:
+    return int(lib().attn_decode_workspace_states(num_heads, kv_len))
+
+
+def rope_tables(max_seq_len: int, head_dim: int, rope_theta: float):
+    """Host fp16 cos/sin tables [max_seq_len, head_dim/2] (rope_cache.hpp:48-76),
+    returned as CPU int16 tensors holding fp16 bits viewed as float16."""
+    half = head_dim // 2
+    cos = torch.empty(max_seq_len * half, dtype=torch.float16)
+    sin = torch.empty(max_seq_len * half, dtype=torch.float16)
+    _check(lib().attn_rope_tables(cos.data_ptr(), sin.data_ptr(), max_seq_len, head_dim,
+                                  float(rope_theta)), "attn_rope_tables")
+    return cos.view(max_seq_len, half), sin.view(max_seq_len, half)
+
+
+def rope_store_kv(q, k, v, k_cache, v_cache, cos, sin, seq_len, num_heads, num_kv_heads,
+                  head_dim, q_stride, k_stride, start_pos, apply_rotation, stream=None):
+    """launch_rope_and_store_kv (kernels.hpp:62-79).  Tensor or int pointers."""
+    rc = lib().attn_rope_store_kv(_ptr(q), _ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache),
+                                  _ptr(cos), _ptr(sin), seq_len, num_heads, num_kv_heads,
+                                  head_dim, q_stride, k_stride, start_pos,
+                                  1 if apply_rotation else 0, _stream(stream))
+    _check(rc, "attn_rope_store_kv")
+
+
+def rope(q, k, cos, sin, seq_len, num_heads, num_kv_heads, head_dim, q_stride, k_stride,
+         start_pos=0, stream=None):
+    """launch_rope (kernels.hpp:47-59)."""
+    rc = lib().attn_rope(_ptr(q), _ptr(k), _ptr(cos), _ptr(sin), seq_len, num_heads,
+                         num_kv_heads, head_dim, q_stride, k_stride, start_pos, _stream(stream))
+    _check(rc, "attn_rope")
+
+
+def prefill(q, k, v, out, seq_len, num_heads, num_kv_heads, head_dim, q_stride=0,
+            kv_stride=0, stream=None):
+    """launch_causal_attention_prefill (kernels.hpp:88-99)."""
+    rc = lib().attn_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(out), seq_len, num_heads,
+                            num_kv_heads, head_dim, q_stride, kv_stride, _stream(stream))
+    _check(rc, "attn_prefill")
+
+
+def decode(q, k_cache, v_cache, out, partial_out, partial_max, partial_sum, query_len,
+           kv_len, start_pos, num_heads, num_kv_heads, head_dim, q_stride=0, kv_stride=0,
+           stream=None):
+    """launch_causal_attention_decode[_vectorized] (kernels.hpp:104-146)."""
+    rc = lib().attn_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out),
+                           _ptr(partial_out), _ptr(partial_max), _ptr(partial_sum), query_len,
+                           kv_len, start_pos, num_heads, num_kv_heads, head_dim, q_stride,
+                           kv_stride, _stream(stream), None, None)
+    _check(rc, "attn_decode")
+
+
+def decode_plan(kv_len, num_heads, num_kv_heads, head_dim, kv_stride=0, q=None, k=None,
+                v=None):
+    out = (ctypes.c_uint32 * 4)()
+    rc = lib().attn_decode_plan(kv_len, num_heads, num_kv_heads, head_dim, kv_stride,
+                                _ptr(q) or 256, _ptr(k) or 256, _ptr(v) or 256, out)
+    _check(rc, "attn_decode_plan")
+    return {"path": out[0], "nsplit": out[1], "chunk": out[2], "block": out[3]}
+
+
+def prefill_plan(q, k, v, out, num_heads, num_kv_heads, head_dim, q_stride=0, kv_stride=0):
+    return int(lib().attn_prefill_plan(_ptr(q), _ptr(k), _ptr(v), _ptr(out), num_heads,
+                                       num_kv_heads, head_dim, q_stride, kv_stride))
+
+
+def decode_workspace(num_heads: int, kv_len: int, head_dim: int, device="cuda"):
+    """Allocate the reference-sized decode workspace (model_inference.hpp:192-198)."""
+    states = decode_workspace_states(num_heads, kv_len)
+    return (torch.empty(states * head_dim, dtype=torch.float32, device=device),
+            torch.empty(states, dtype=torch.float32, device=device),
+            torch.empty(states, dtype=torch.float32, device=device))
+
+
+class KVCache:
+    """Device KV cache with the reference layout (kv_cache.hpp:8-83): one buffer for
+    all layers; layer l holds K [S][Hkv*D] then V [S][Hkv*D]."""
+
+    def __init__(self, num_layers, max_seq_len, num_kv_heads, head_dim, device="cuda",
+                 fill=None):
+        self.num_layers = num_layers
+        self.max_seq_len = max_seq_len
+        self.kv_dim = num_kv_heads * head_dim
+        total = 2 * self.kv_dim * max_seq_len * num_layers
+        if fill is None:
+            self.buffer = torch.empty(total, dtype=torch.float16, device=device)
+        else:
+            self.buffer = torch.full((total,), fill, dtype=torch.float16, device=device)
+        self.cached_len = 0
+
+    def layer_stride(self):
+        return 2 * self.kv_dim * self.max_seq_len
+
+    def k(self, layer):
+        o = layer * self.layer_stride()
+        return self.buffer[o:o + self.max_seq_len * self.kv_dim].view(self.max_seq_len, self.kv_dim)
+
+    def v(self, layer):
+        o = layer * self.layer_stride() + self.max_seq_len * self.kv_dim
+        return self.buffer[o:o + self.max_seq_len * self.kv_dim].view(self.max_seq_len, self.kv_dim)
+
+    def set_cached_len(self, n):
+        if n > self.max_seq_len:  # kv_cache.hpp:40-45
+            raise IndexError(f"KV cache capacity exceeded: requested {n} tokens, capacity "
+                             f"{self.max_seq_len}")
+        self.cached_len = n
+
+
+def scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

@@ -1,0 +1,110 @@
+"""The C ABI without a GPU: the library loads, exports every entry point that
+include/attn_mi355x.h declares, its host-side pieces (RoPE tables, workspace
+sizing) match the oracle, and the reference's silent no-op shapes return 0
+without touching a device.  CPU only."""
+import ctypes
+import pathlib
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "attn_mi355x.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(attn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_reference_entry_points():
+    names = declared_symbols()
+    for n in ("attn_rope_store_kv", "attn_rope", "attn_update_rope_node", "attn_prefill",
+              "attn_decode", "attn_update_decode_node", "attn_update_merge_node"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(attn):
+    lib = attn.lib()
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert sorted(attn.exported_symbols()) == declared_symbols()
+    assert b"gfx950" in lib.attn_version()
+
+
+def test_library_is_gfx950_code():
+    so = (ROOT / "llm-inference_amd" / "lib" / "libattn_mi355x.so").read_bytes()
+    assert b"gfx950" in so
+    assert b"gfx942" not in so and b"gfx1030" not in so
+
+
+@pytest.mark.parametrize("S,D,theta", [(300, 128, 5.0e6), (40000, 128, 5.0e6), (64, 32, 1.0e4)])
+def test_host_rope_tables_bitexact_vs_oracle(attn, S, D, theta):
+    c, s = attn.rope_tables(S, D, theta)
+    oc, os_ = oracle.rope_tables(S, D, theta)
+    assert np.array_equal(c.numpy().view(np.uint16), oc)
+    assert np.array_equal(s.numpy().view(np.uint16), os_)
+
+
+def test_workspace_states_formula(attn):
+    # model_inference.hpp:192-198 and kernels.hpp:103 (KV_CHUNK = 12)
+    for L in (1, 12, 13, 254, 32768, 32769):
+        assert attn.decode_workspace_states(16, L) == 16 * ((L + 11) // 12)
+
+
+def test_noop_shapes_touch_nothing(attn):
+    lib = attn.lib()
+    # launch_rope_and_store_kv: seq_len == 0 (rope.hip.cpp:156)
+    assert lib.attn_rope_store_kv(None, None, None, None, None, None, None, 0, 16, 4, 128, 0, 0,
+                                  0, 1, None) == 0
+    # prefill: seq_len == 0, num_kv_heads == 0, Hq % Hkv != 0 (causal_attention.hip.cpp:392-399)
+    for n, hq, hkv in ((0, 16, 4), (8, 16, 0), (8, 16, 3)):
+        assert lib.attn_prefill(None, None, None, None, n, hq, hkv, 128, 0, 0, None) == 0
+    # decode: query_len == 0, kv_len == 0, num_kv_heads == 0, head_dim == 0,
+    # Hq % Hkv != 0 (:860-866, :945-946)
+    for ql, L, hq, hkv, d in ((0, 5, 16, 4, 128), (1, 0, 16, 4, 128), (1, 5, 16, 0, 128),
+                              (1, 5, 16, 4, 0), (1, 5, 16, 3, 128)):
+        assert lib.attn_decode(None, None, None, None, None, None, None, ql, L, 0, hq, hkv, d, 0,
+                               0, None, None, None) == 0
+
+
+def test_invalid_arguments_are_errors(attn):
+    lib = attn.lib()
+    # odd head_dim cannot be split into rotation pairs
+    assert lib.attn_rope_store_kv(None, None, None, None, None, None, None, 1, 16, 4, 127, 0, 0,
+                                  0, 1, None) != 0
+    # NoPE copy without a cache
+    assert lib.attn_rope_store_kv(None, None, None, None, None, None, None, 1, 16, 4, 128, 0, 0,
+                                  0, 0, None) != 0
+    assert lib.attn_set_option(b"no_such_option", 1) == -1
+    assert lib.attn_update_decode_node(None, None, 0) != 0
+
+
+def test_decode_plan_respects_workspace_capacity(attn):
+    # whatever the split plan, partial states + counters fit in the
+    # reference-sized workspace Hq * ceil(L / 12)
+    for L in (1, 12, 13, 100, 129, 254, 1000, 4096, 32768, 65536, 131072):
+        for hq, hkv in ((16, 4), (4, 4), (2, 1), (16, 1), (32, 8)):
+            p = attn.decode_plan(L, hq, hkv, 128)
+            cap = hq * ((L + 11) // 12)
+            assert p["path"] in (1, 2)
+            assert p["nsplit"] >= 1 and p["chunk"] * p["nsplit"] >= L
+            assert (p["nsplit"] - 1) * p["chunk"] < L  # no empty split
+            if p["nsplit"] > 1:
+                assert hq * p["nsplit"] + 2 * hkv + 2 <= cap
+    # head_dim != 128 or an odd stride takes the generic kernel
+    assert attn.decode_plan(257, 4, 2, 32)["path"] == 0
+    assert attn.decode_plan(257, 4, 2, 128, kv_stride=2 * 128 + 17)["path"] == 0
+
+
+def test_prefill_plan(attn):
+    a = 4096
+    assert attn.prefill_plan(a, a, a, a, 16, 4, 128, 3072, 512) == 1
+    assert attn.prefill_plan(a, a, a, a, 16, 4, 64, 0, 0) == 0       # D != 128
+    assert attn.prefill_plan(a, a, a, a, 16, 16, 128, 0, 0) == 0     # group of 1
+    assert attn.prefill_plan(a, a, a, a, 16, 4, 128, 3075, 512) == 0  # unaligned stride
+    assert attn.prefill_plan(a + 2, a, a, a, 16, 4, 128, 0, 0) == 0   # unaligned pointer

@@ -1,0 +1,217 @@
+"""Flash-Decode on the GPU vs the oracle.
+
+* The reference's own known-answer test (test_causal_attention.cpp:152-228):
+  closed-form inputs, head_dim {32, 128}, kv_heads {1, 2, 4}, lengths
+  {1, 12, 13, 37, 257}, padded odd strides, output guards; tolerance 2e-3/2e-3.
+* SmolLM3 shapes (16 query heads, 4 KV heads, D 128) at L up to 65536 with
+  N(0,1) inputs and sentinel cache rows past L: |a - e| <= 2e-3 + 1e-2 |e|
+  against the fp64 oracle.
+* The result must not depend on the split plan; the workspace is only written
+  inside the reference-sized capacity; graph nodes re-planned by
+  update_causal_attention_decode_node replay bit-identically to eager launches.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import assert_close
+
+pytestmark = pytest.mark.gpu
+
+GUARD = np.float16(-123.0).view(np.uint16)
+
+
+def dev(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.float16)).to(device)
+
+
+def host(t):
+    return t.detach().cpu().numpy().view(np.uint16)
+
+
+def workspace(attn, device, Hq, L, D, guard_floats=64):
+    """Reference-sized workspace (Hq*ceil(L/12) states) inside larger buffers
+    whose tails are NaN canaries."""
+    states = attn.decode_workspace_states(Hq, L)
+    po = torch.full((states * D + guard_floats,), float("nan"), device=device)
+    pm = torch.full((states + guard_floats,), float("nan"), device=device)
+    ps = torch.full((states + guard_floats,), float("nan"), device=device)
+    return po, pm, ps, states
+
+
+def check_workspace_tails(ws, D):
+    po, pm, ps, states = ws
+    assert torch.isnan(po[states * D:]).all()
+    assert torch.isnan(pm[states:]).all()
+    assert torch.isnan(ps[states:]).all()
+
+
+def run_decode(attn, device, q, k, v, L, Hq, Hkv, D, kv_stride=0, out_offset=1):
+    q_dim = Hq * D
+    dq, dk, dv = dev(q, device), dev(k, device), dev(v, device)
+    out = torch.from_numpy(np.full(q_dim + 2 * out_offset, GUARD, dtype=np.uint16)
+                           .view(np.float16)).to(device)
+    ws = workspace(attn, device, Hq, L, D)
+    attn.decode(dq, dk, dv, out.data_ptr() + 2 * out_offset, ws[0], ws[1], ws[2], 1, L, L - 1,
+                Hq, Hkv, D, 0, kv_stride)
+    torch.cuda.synchronize()
+    got = host(out)
+    assert np.all(got[:out_offset] == GUARD) and np.all(got[out_offset + q_dim:] == GUARD)
+    check_workspace_tails(ws, D)
+    return got[out_offset:out_offset + q_dim]
+
+
+@pytest.mark.parametrize("head_dim", [32, 128])
+@pytest.mark.parametrize("kv_heads", [1, 2, 4])
+def test_reference_flash_decode_kat(attn, gpu, golden, head_dim, kv_heads):
+    g = golden("kat_flash_decode.npz")
+    heads = 4
+    for length in (1, 12, 13, 37, 257):
+        for padded in (0, 1):
+            print(f"[case] KAT D={head_dim} kv={kv_heads} len={length} pad={padded}", flush=True)
+            stride = kv_heads * head_dim + (17 if padded else 0)
+            q, k, v = oracle.kat_inputs(heads, head_dim, kv_heads, length, stride)
+            got = run_decode(attn, gpu, q, k, v, length, heads, kv_heads, head_dim,
+                             kv_stride=stride if padded else 0)
+            key = f"d{head_dim}_kv{kv_heads}_len{length}_pad{padded}"
+            assert_close(got, g[key + "_expected"], 2e-3, 2e-3, key)
+
+
+def smol_inputs(L, seed, cap_extra=2, sigma=1.0):
+    Hq, Hkv, D = 16, 4, 128
+    rng = np.random.default_rng(seed)
+    q = (rng.standard_normal(Hq * D) * sigma).astype(np.float16).view(np.uint16)
+    k = np.full((L + cap_extra) * Hkv * D, np.float16(123.0).view(np.uint16), dtype=np.uint16)
+    v = k.copy()
+    k[:L * Hkv * D] = (rng.standard_normal(L * Hkv * D) * sigma).astype(np.float16).view(np.uint16)
+    v[:L * Hkv * D] = (rng.standard_normal(L * Hkv * D) * sigma).astype(np.float16).view(np.uint16)
+    return q, k, v
+
+
+def expected(q, k, v, L, Hq=16, Hkv=4, D=128):
+    _, e32 = oracle.attention(q, k, v, 1, Hq, Hkv, D, Hq * D, Hkv * D, L, L - 1, causal=False)
+    return e32.reshape(-1)
+
+
+@pytest.mark.parametrize("L", [1, 2, 12, 13, 127, 128, 129, 254, 255, 1000, 4096, 16384, 32768,
+                               65536])
+def test_decode_smollm3_vs_oracle(attn, gpu, L):
+    print(f"[case] decode L={L} plan={attn.decode_plan(L, 16, 4, 128)}", flush=True)
+    q, k, v = smol_inputs(L, seed=3)
+    got = run_decode(attn, gpu, q, k, v, L, 16, 4, 128)
+    assert_close(got, expected(q, k, v, L), 2e-3, 1e-2, f"L={L}")
+
+
+def test_decode_golden_fixtures(attn, gpu, golden):
+    g = golden("attention.npz")
+    for case in ("decode_a", "decode_b", "decode_c"):
+        q, k, v, e = (g[f"{case}_{x}"] for x in ("q", "k", "v", "expected"))
+        _, Hq, D = q.shape
+        L, Hkv, _ = k.shape
+        print(f"[case] decode golden {case} L={L} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+        got = run_decode(attn, gpu, q.reshape(-1), k.reshape(-1), v.reshape(-1), L, Hq, Hkv, D)
+        assert_close(got, e.reshape(-1), 2e-3, 2e-3, case)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 64, 256])
+def test_decode_independent_of_split_plan(attn, gpu, splits):
+    L = 20000
+    q, k, v = smol_inputs(L, seed=9)
+    e = expected(q, k, v, L)
+    attn.set_option("decode_splits", splits)
+    try:
+        print(f"[case] decode L={L} splits={splits} plan={attn.decode_plan(L, 16, 4, 128)}",
+              flush=True)
+        got = run_decode(attn, gpu, q, k, v, L, 16, 4, 128)
+    finally:
+        attn.set_option("decode_splits", 0)
+    assert_close(got, e, 2e-3, 1e-2, f"splits={splits}")
+
+
+def test_decode_eight_wave_variant_and_generic(attn, gpu):
+    L = 5000
+    q, k, v = smol_inputs(L, seed=10)
+    e = expected(q, k, v, L)
+    for opt, val in (("decode_waves", 8), ("decode_force_generic", 1)):
+        attn.set_option(opt, val)
+        try:
+            print(f"[case] decode {opt}={val} plan={attn.decode_plan(L, 16, 4, 128)}", flush=True)
+            got = run_decode(attn, gpu, q, k, v, L, 16, 4, 128)
+        finally:
+            attn.set_option(opt, 0)
+        assert_close(got, e, 2e-3, 1e-2, opt)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(16, 16), (8, 1), (32, 2), (12, 4)])
+def test_decode_other_group_sizes(attn, gpu, Hq, Hkv):
+    L, D = 3000, 128
+    rng = np.random.default_rng(Hq * 100 + Hkv)
+    q = rng.standard_normal(Hq * D).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal(L * Hkv * D).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal(L * Hkv * D).astype(np.float16).view(np.uint16)
+    print(f"[case] decode Hq={Hq} Hkv={Hkv} plan={attn.decode_plan(L, Hq, Hkv, D)}", flush=True)
+    got = run_decode(attn, gpu, q, k, v, L, Hq, Hkv, D)
+    assert_close(got, expected(q, k, v, L, Hq, Hkv, D), 2e-3, 1e-2, f"{Hq}/{Hkv}")
+
+
+def test_decode_closed_forms(attn, gpu):
+    # one key: the output is V[0] bit for bit; identical keys: the mean of V
+    q, k, v = smol_inputs(1, seed=11)
+    got = run_decode(attn, gpu, q, k, v, 1, 16, 4, 128)
+    vv = v[:512].reshape(4, 128)
+    assert np.array_equal(got.reshape(16, 128), np.repeat(vv, 4, axis=0))
+    L = 777
+    q, k, v = smol_inputs(L, seed=12)
+    k[:L * 512] = np.tile(k[:512], L)
+    got = run_decode(attn, gpu, q, k, v, L, 16, 4, 128)
+    mean = v[:L * 512].view(np.float16).astype(np.float64).reshape(L, 4, 128).mean(axis=0)
+    assert_close(got, np.repeat(mean, 4, axis=0).reshape(-1), 2e-3, 2e-3, "mean of V")
+
+
+def test_decode_graph_node_update(attn, gpu):
+    """model_inference.hpp:96-126: capture once, then patch kv_len with
+    update_causal_attention_decode_node / update_merge_attention_decode_node
+    and replay.  Each replay equals an eager launch bit for bit and the oracle
+    within tolerance; eager work runs between replays."""
+    import ctypes
+
+    from attn_mi355x import hipgraph
+    Lmax = 40000
+    q, k, v = smol_inputs(Lmax, seed=13)
+    dq, dk, dv = dev(q, gpu), dev(k, gpu), dev(v, gpu)
+    states = attn.decode_workspace_states(16, Lmax)
+    po = torch.empty(states * 128, device=gpu)
+    pm = torch.empty(states, device=gpu)
+    ps = torch.empty(states, device=gpu)
+    out_g = torch.empty(2048, dtype=torch.float16, device=gpu)
+    out_e = torch.empty(2048, dtype=torch.float16, device=gpu)
+    po2, pm2, ps2 = po.clone(), pm.clone(), ps.clone()
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    L0 = 100
+    anode, mnode = ctypes.c_void_p(), ctypes.c_void_p()
+    with torch.cuda.stream(stream):
+        hipgraph.begin_capture(sp)
+        rc = attn.lib().attn_decode(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                    out_g.data_ptr(), po.data_ptr(), pm.data_ptr(), ps.data_ptr(),
+                                    1, L0, L0 - 1, 16, 4, 128, 3072, 512, sp,
+                                    ctypes.byref(anode), ctypes.byref(mnode))
+        assert rc == 0
+        graph, exe = hipgraph.end_capture(sp)
+    try:
+        for L in (100, 101, 254, 4096, 4097, 33000, 39999, 100):
+            assert attn.lib().attn_update_decode_node(exe, anode, L) == 0
+            assert attn.lib().attn_update_merge_node(exe, mnode, L) == 0
+            for rep in range(2):
+                out_g.fill_(0.0)
+                torch.cuda.synchronize()
+                hipgraph.launch(exe, sp)
+                hipgraph.synchronize(sp)
+                attn.decode(dq, dk, dv, out_e, po2, pm2, ps2, 1, L, L - 1, 16, 4, 128, 0, 512)
+                torch.cuda.synchronize()
+                print(f"[case] decode graph L={L} replay {rep}", flush=True)
+                assert np.array_equal(host(out_g), host(out_e)), (L, rep)
+            assert_close(host(out_g), expected(q, k, v, L), 2e-3, 1e-2, f"graph L={L}")
+    finally:
+        hipgraph.destroy(graph, exe)

@@ -1,0 +1,168 @@
+"""Causal GQA prefill on the GPU vs the oracle (and, at 8192 tokens, vs a torch
+fp32 reference computed on the GPU).
+
+Engine layout as in model_inference.hpp:272-293: Q read in place from the fused
+[N, 3072] QKV buffer (q_stride 3072), K/V from the KV cache (kv_stride 512)
+whose rows past N hold sentinel 123.0 (test_causal_attention.cpp:31-50); the
+test_qkv_gemm.cpp:86-116 chain reads K/V straight from the fused buffer.
+Tolerance: |a - e| <= 2e-3 + 1e-2 |e| against the fp64 oracle."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.float16)).to(device)
+
+
+def host(t):
+    return t.detach().cpu().numpy().view(np.uint16)
+
+
+def engine_inputs(N, seed, sigma=1.0, Hq=16, Hkv=4, D=128):
+    rng = np.random.default_rng(seed)
+    stride = Hq * D + 2 * Hkv * D
+    qkv = (rng.standard_normal(N * stride) * sigma).astype(np.float16).view(np.uint16)
+    cache = np.full(2 * (N + 2) * Hkv * D, np.float16(123.0).view(np.uint16), dtype=np.uint16)
+    rows = qkv.reshape(N, stride)
+    kc = cache[:(N + 2) * Hkv * D].reshape(N + 2, Hkv * D)
+    vc = cache[(N + 2) * Hkv * D:].reshape(N + 2, Hkv * D)
+    kc[:N] = rows[:, Hq * D:Hq * D + Hkv * D]
+    vc[:N] = rows[:, Hq * D + Hkv * D:]
+    return qkv, cache, stride
+
+
+def run_prefill(attn, device, qkv, cache, N, stride, Hq=16, Hkv=4, D=128, from_cache=True):
+    kv_dim = Hkv * D
+    d_qkv, d_cache = dev(qkv, device), dev(cache, device)
+    out = torch.empty(N * Hq * D, dtype=torch.float16, device=device)
+    b, cb = d_qkv.data_ptr(), d_cache.data_ptr()
+    if from_cache:
+        attn.prefill(b, cb, cb + 2 * (N + 2) * kv_dim, out, N, Hq, Hkv, D, stride, kv_dim)
+    else:
+        attn.prefill(b, b + 2 * Hq * D, b + 2 * (Hq * D + kv_dim), out, N, Hq, Hkv, D, stride,
+                     stride)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(d_qkv), qkv) and np.array_equal(host(d_cache), cache)
+    return host(out)
+
+
+def oracle_prefill(qkv, cache, N, stride, Hq=16, Hkv=4, D=128, rows=None):
+    kv_dim = Hkv * D
+    k = cache[:(N + 2) * kv_dim]
+    v = cache[(N + 2) * kv_dim:]
+    _, e32 = oracle.attention(qkv, k, v, N, Hq, Hkv, D, stride, kv_dim, N, causal=True,
+                              rows=rows)
+    return e32
+
+
+@pytest.mark.parametrize("N", [1, 2, 31, 63, 64, 65, 128, 200, 254])
+def test_prefill_engine_layout(attn, gpu, N):
+    qkv, cache, stride = engine_inputs(N, seed=N)
+    print(f"[case] prefill N={N} path={attn.prefill_plan(4096, 4096, 4096, 4096, 16, 4, 128, stride, 512)}",
+          flush=True)
+    got = run_prefill(attn, gpu, qkv, cache, N, stride)
+    assert_close(got, oracle_prefill(qkv, cache, N, stride).reshape(-1), 2e-3, 1e-2, f"N={N}")
+
+
+def test_prefill_fused_buffer_chain(attn, gpu):
+    # test_qkv_gemm.cpp:86-116: K/V read from the interleaved GEMM output
+    N = 254
+    qkv, cache, stride = engine_inputs(N, seed=77)
+    got = run_prefill(attn, gpu, qkv, cache, N, stride, from_cache=False)
+    _, e32 = oracle.attention(qkv, qkv[2048:], qkv[2560:], N, 16, 4, 128, stride, stride, N,
+                              causal=True)
+    assert_close(got, e32.reshape(-1), 2e-3, 1e-2, "chain")
+
+
+def test_prefill_golden_fixtures(attn, gpu, golden):
+    g = golden("attention.npz")
+    for case in ("prefill_a", "prefill_b", "prefill_c"):
+        q, k, v, e = (g[f"{case}_{x}"] for x in ("q", "k", "v", "expected"))
+        N, Hq, D = q.shape
+        Hkv = k.shape[1]
+        print(f"[case] prefill golden {case} N={N} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+        out = torch.empty(N * Hq * D, dtype=torch.float16, device=gpu)
+        attn.prefill(dev(q, gpu), dev(k, gpu), dev(v, gpu), out, N, Hq, Hkv, D)
+        torch.cuda.synchronize()
+        assert_close(host(out), e.reshape(-1), 2e-3, 2e-3, case)
+
+
+def test_prefill_8192_vs_oracle_rows_and_torch(attn, gpu):
+    """C4: 8192 tokens, N(0, 0.5).  Sampled rows against the fp64 oracle, every
+    row against a torch fp32 reference on the GPU (math path, row blocks)."""
+    N, Hq, Hkv, D = 8192, 16, 4, 128
+    qkv, cache, stride = engine_inputs(N, seed=4, sigma=0.5)
+    print("[case] prefill N=8192", flush=True)
+    got = run_prefill(attn, gpu, qkv, cache, N, stride)
+    rows = np.unique(np.concatenate([np.arange(0, 70), np.arange(N - 70, N),
+                                     np.arange(63, N, 512), np.arange(64, N, 1021)]))
+    e_rows = oracle_prefill(qkv, cache, N, stride, rows=rows)
+    got3 = got.reshape(N, Hq, D)
+    assert_close(got3[rows].reshape(-1), e_rows.reshape(-1), 2e-3, 1e-2, "oracle rows")
+    # torch fp32 reference for all rows
+    x = torch.from_numpy(qkv.view(np.float16)).to(gpu).view(N, stride).float()
+    q = x[:, :Hq * D].view(N, Hq, D).transpose(0, 1).contiguous()
+    k = x[:, Hq * D:Hq * D + Hkv * D].view(N, Hkv, D).transpose(0, 1)
+    v = x[:, Hq * D + Hkv * D:].view(N, Hkv, D).transpose(0, 1)
+    k = k.repeat_interleave(Hq // Hkv, dim=0).contiguous()
+    v = v.repeat_interleave(Hq // Hkv, dim=0).contiguous()
+    ref = torch.empty(Hq, N, D, device=gpu)
+    for r0 in range(0, N, 1024):
+        r1 = r0 + 1024
+        s = torch.matmul(q[:, r0:r1], k[:, :r1].transpose(1, 2).contiguous()) / np.sqrt(D)
+        mask = torch.arange(r1, device=gpu)[None, :] > torch.arange(r0, r1, device=gpu)[:, None]
+        s.masked_fill_(mask[None], float("-inf"))
+        ref[:, r0:r1] = torch.matmul(torch.softmax(s, dim=-1), v[:, :r1])
+    ref = ref.transpose(0, 1).contiguous().cpu().numpy().reshape(-1)
+    assert_close(got, ref, 2e-3, 1e-2, "torch fp32")
+
+
+def test_prefill_prefix_invariance(attn, gpu):
+    # row t depends only on rows <= t: a prefill of N tokens and of a prefix of
+    # N' tokens agree bit for bit on the first N' rows
+    N = 700
+    qkv, cache, stride = engine_inputs(N, seed=21)
+    full = run_prefill(attn, gpu, qkv, cache, N, stride).reshape(N, -1)
+    for Np in (1, 64, 65, 333):
+        q2, c2, _ = engine_inputs(N, seed=21)
+        c2 = np.concatenate([c2[:(N + 2) * 512].reshape(N + 2, 512)[:Np + 2].reshape(-1),
+                             c2[(N + 2) * 512:].reshape(N + 2, 512)[:Np + 2].reshape(-1)])
+        part = run_prefill(attn, gpu, q2[:Np * stride], c2, Np, stride).reshape(Np, -1)
+        assert np.array_equal(part, full[:Np]), Np
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,extra", [(16, 4, 64, 0), (16, 16, 128, 0), (8, 2, 128, 8),
+                                            (16, 4, 128, 3), (6, 2, 32, 0)])
+def test_prefill_generic_shapes(attn, gpu, Hq, Hkv, D, extra):
+    N = 97
+    rng = np.random.default_rng(D + Hq + extra)
+    stride = Hq * D + 2 * Hkv * D + extra
+    qkv = rng.standard_normal(N * stride).astype(np.float16).view(np.uint16)
+    path = attn.prefill_plan(4096, 4096, 4096, 4096, Hq, Hkv, D, stride, stride)
+    print(f"[case] prefill Hq={Hq} Hkv={Hkv} D={D} extra={extra} path={path}", flush=True)
+    d = dev(qkv, gpu)
+    out = torch.empty(N * Hq * D, dtype=torch.float16, device=gpu)
+    b = d.data_ptr()
+    attn.prefill(b, b + 2 * Hq * D, b + 2 * (Hq * D + Hkv * D), out, N, Hq, Hkv, D, stride,
+                 stride)
+    torch.cuda.synchronize()
+    _, e32 = oracle.attention(qkv, qkv[Hq * D:], qkv[Hq * D + Hkv * D:], N, Hq, Hkv, D, stride,
+                              stride, N, causal=True)
+    assert_close(host(out), e32.reshape(-1), 2e-3, 1e-2, f"{Hq}/{Hkv}/{D}")
+
+
+def test_prefill_forced_generic_matches_oracle(attn, gpu):
+    N = 150
+    qkv, cache, stride = engine_inputs(N, seed=5)
+    attn.set_option("prefill_force_generic", 1)
+    try:
+        got = run_prefill(attn, gpu, qkv, cache, N, stride)
+    finally:
+        attn.set_option("prefill_force_generic", 0)
+    assert_close(got, oracle_prefill(qkv, cache, N, stride).reshape(-1), 2e-3, 1e-2, "generic")
