@@ -75,8 +75,10 @@ int attn_prefill(const attn_f16_t* q, const attn_f16_t* k, const attn_f16_t* v,
  * and start_pos are accepted and unused, as in the reference); out is packed
  * [num_heads][head_dim].  partial_out/max/sum are caller-owned workspace of at
  * least num_heads*ceil(kv_len/ATTN_KV_CHUNK) states (partial_out: x head_dim
- * floats); their contents are private to this library.  Exactly one kernel is
- * enqueued; when capturing, *attention_node and *merge_node both receive it.
+ * floats); their contents are private to this library.  For head_dim 128 two
+ * kernels are enqueued, the split kernel (*attention_node) and the partial
+ * merge (*merge_node), as in the reference; other shapes enqueue one generic
+ * kernel and both handles receive it.
  * Replaces launch_causal_attention_decode (kernels.hpp:104-123) and
  * launch_causal_attention_decode_vectorized (kernels.hpp:127-146;
  * causal_attention.hip.cpp:840-972). */
@@ -91,10 +93,10 @@ int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t
  * (kernels.hpp:190-194; causal_attention.hip.cpp:975-1001). */
 int attn_update_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len);
 
-/* Companion of attn_update_decode_node for the merge node.  The merge runs
- * inside the decode kernel, so for nodes returned by attn_decode this is a
- * no-op that validates the node.  Replaces update_merge_attention_decode_node
- * (kernels.hpp:148-152; causal_attention.hip.cpp:1003-1026). */
+/* Re-point a captured merge node at a new kv_len (its split count).  For the
+ * single-kernel generic path this is a no-op.  Replaces
+ * update_merge_attention_decode_node (kernels.hpp:148-152;
+ * causal_attention.hip.cpp:1003-1026). */
 int attn_update_merge_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len);
 
 /* Workspace states a caller must provide for kv_len keys:
@@ -109,9 +111,9 @@ int attn_rope_tables(attn_f16_t* cos_out, attn_f16_t* sin_out, size_t max_seq_le
                      size_t head_dim, float rope_theta);
 
 /* Introspection for tests and benchmarks: the decode plan chosen for a shape
- * on the current device.  out[0] = path (0 generic, 1 MFMA 4-wave, 2 MFMA
- * 8-wave), out[1] = splits per KV head, out[2] = keys per split,
- * out[3] = threads per workgroup. */
+ * on the current device.  out[0] = path (0 generic; 1, 2, 3 = MFMA split
+ * kernel serving 4, 2, 1 KV heads per workgroup), out[1] = splits of the
+ * context, out[2] = keys per split, out[3] = threads per workgroup. */
 int attn_decode_plan(size_t kv_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
                      size_t kv_stride, const void* q, const void* k_cache,
                      const void* v_cache, uint32_t out[4]);
@@ -122,9 +124,8 @@ int attn_prefill_plan(const void* q, const void* k, const void* v, const void* o
                       size_t kv_stride);
 
 /* Process-wide switches for tests and benchmarks (not needed in production):
- * "decode_force_generic", "decode_splits" (0 = automatic), "decode_waves"
- * (4 or 8; 0 = automatic), "prefill_force_generic".  Returns 0 or -1 for an
- * unknown name. */
+ * "decode_force_generic", "decode_splits" (0 = automatic),
+ * "prefill_force_generic".  Returns 0 or -1 for an unknown name. */
 int attn_set_option(const char* name, long value);
 
 /* Library build identification (static string). */

@@ -72,7 +72,6 @@ int attn_set_option(const char* name, long value) {
     if (!std::strcmp(name, "decode_force_generic")) which = kOptDecodeForceGeneric;
     else if (!std::strcmp(name, "decode_splits")) which = kOptDecodeSplits;
     else if (!std::strcmp(name, "prefill_force_generic")) which = kOptPrefillForceGeneric;
-    else if (!std::strcmp(name, "decode_waves")) which = kOptDecodeWaves;
     if (which < 0) return -1;
     g_options[which].store(value, std::memory_order_relaxed);
     return 0;
@@ -257,7 +256,9 @@ int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t
     const DecodePlan p = plan_decode((uint32_t)kv_len, (uint32_t)num_heads,
                                      (uint32_t)num_kv_heads, (uint32_t)head_dim, kvs, q,
                                      k_cache, v_cache, device);
+    hipGraphNode_t node = nullptr;
     if (p.path == 0) {
+        // one kernel: both node handles name it (the merge patcher is a no-op)
         GenericAttnArgs g{};
         g.q = reinterpret_cast<const f16*>(q);
         g.k = reinterpret_cast<const f16*>(k_cache);
@@ -273,78 +274,87 @@ int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t
         g.causal = 0;
         g.scale_log2 = scale_log2_for(head_dim);
         e = launch_generic_attention(g, stream);
-    } else {
-        if (!partial_out || !partial_max || !partial_sum) return (int)hipErrorInvalidValue;
-        DecodeArgs a{};
-        a.q = reinterpret_cast<const f16*>(q);
-        a.k = reinterpret_cast<const f16*>(k_cache);
-        a.v = reinterpret_cast<const f16*>(v_cache);
-        a.out = reinterpret_cast<f16*>(out);
-        a.part_out = partial_out;
-        a.part_max = partial_max;
-        a.part_sum = partial_sum;
-        a.kv_stride = kvs;
-        a.kv_len = (uint32_t)kv_len;
-        a.num_heads = (uint32_t)num_heads;
-        a.num_kv_heads = (uint32_t)num_kv_heads;
-        a.group = (uint32_t)(num_heads / num_kv_heads);
-        a.head_dim = (uint32_t)head_dim;
-        a.scale_log2 = scale_log2_for(head_dim);
-        replan_decode(a, p.path, device);
-        e = launch_decode_kernel(a, p, stream);
-    }
-    if (e != hipSuccess) return (int)e;
-    if (attention_node || merge_node) {
-        hipGraphNode_t node = nullptr;
-        e = captured_node(stream, &node);
         if (e != hipSuccess) return (int)e;
-        if (attention_node) *attention_node = node;
-        if (merge_node) *merge_node = node;
+        if (attention_node || merge_node) {
+            e = captured_node(stream, &node);
+            if (e != hipSuccess) return (int)e;
+            if (attention_node) *attention_node = node;
+            if (merge_node) *merge_node = node;
+        }
+        return 0;
+    }
+    if (!partial_out || !partial_max || !partial_sum) return (int)hipErrorInvalidValue;
+    DecodeArgs a{};
+    a.q = reinterpret_cast<const f16*>(q);
+    a.k = reinterpret_cast<const f16*>(k_cache);
+    a.v = reinterpret_cast<const f16*>(v_cache);
+    a.out = reinterpret_cast<f16*>(out);
+    a.part_out = partial_out;
+    a.part_max = partial_max;
+    a.part_sum = partial_sum;
+    a.kv_stride = kvs;
+    a.kv_len = (uint32_t)kv_len;
+    a.num_heads = (uint32_t)num_heads;
+    a.num_kv_heads = (uint32_t)num_kv_heads;
+    a.group = (uint32_t)(num_heads / num_kv_heads);
+    a.head_dim = (uint32_t)head_dim;
+    a.scale_log2 = scale_log2_for(head_dim);
+    a.nsplit = p.nsplit;
+    a.chunk = p.chunk;
+    e = launch_decode_split(a, p, stream);
+    if (e != hipSuccess) return (int)e;
+    if (attention_node) {
+        e = captured_node(stream, attention_node);
+        if (e != hipSuccess) return (int)e;
+    }
+    e = launch_decode_merge(a, stream);
+    if (e != hipSuccess) return (int)e;
+    if (merge_node) {
+        e = captured_node(stream, merge_node);
+        if (e != hipSuccess) return (int)e;
     }
     return 0;
 }
 
-int attn_update_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len) {
+static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len,
+                             bool merge) {
     if (kv_len == 0 || !fits_u32(kv_len)) return (int)hipErrorInvalidValue;
     hipKernelNodeParams params{};
     hipError_t e = hipGraphKernelNodeGetParams(node, &params);
     if (e != hipSuccess) return (int)e;
     if (params.func == generic_attention_symbol()) {
+        if (merge) return 0;  // single-kernel path: nothing separate to patch
         GenericAttnArgs g = *reinterpret_cast<const GenericAttnArgs*>(params.kernelParams[0]);
-        if (g.causal) return (int)hipErrorInvalidValue;  // not a decode node
+        if (g.causal) return (int)hipErrorInvalidValue;  // a prefill node, not decode
         g.kv_len = (uint32_t)kv_len;
         void* args[1] = {&g};
         params.kernelParams = args;
         params.extra = nullptr;
         return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
     }
-    int path = 0;
-    if (params.func == decode_kernel_symbol(1)) path = 1;
-    else if (params.func == decode_kernel_symbol(2)) path = 2;
-    else return (int)hipErrorInvalidValue;
+    const bool is_split =
+        params.func == decode_split_symbol(1) || params.func == decode_split_symbol(2);
+    const bool is_merge = params.func == decode_merge_symbol();
+    if ((merge && !is_merge) || (!merge && !is_split)) return (int)hipErrorInvalidValue;
     DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(params.kernelParams[0]);
     int device = 0;
     e = hipGetDevice(&device);
     if (e != hipSuccess) return (int)e;
     a.kv_len = (uint32_t)kv_len;
-    replan_decode(a, path, device);
+    replan_decode(a, device);
     void* args[1] = {&a};
     params.kernelParams = args;
     params.extra = nullptr;
-    params.gridDim.x = a.nsplit;
+    if (!merge) params.gridDim.x = a.nsplit;
     return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
 }
 
+int attn_update_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len) {
+    return patch_decode_node(graph_exec, node, kv_len, false);
+}
+
 int attn_update_merge_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len) {
-    (void)graph_exec;
-    (void)kv_len;
-    hipKernelNodeParams params{};
-    hipError_t e = hipGraphKernelNodeGetParams(node, &params);
-    if (e != hipSuccess) return (int)e;
-    if (params.func == generic_attention_symbol() || params.func == decode_kernel_symbol(1) ||
-        params.func == decode_kernel_symbol(2))
-        return 0;
-    return (int)hipErrorInvalidValue;
+    return patch_decode_node(graph_exec, node, kv_len, true);
 }
 
 }  // extern "C"

@@ -26,6 +26,21 @@ __device__ __forceinline__ void st16(f16* p, f16x8 v) {
     *reinterpret_cast<f16x8*>(p) = v;
 }
 
+// Raw buffer resource over [base, base + bytes): 16-byte loads through it use
+// 32-bit offsets, and any load past `bytes` returns zeros without touching
+// memory (the gfx9 buffer range check), which replaces per-row clamps.
+// dword3 = 0x00020000 selects the 32-bit data format of an untyped buffer.
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+__device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+__device__ __forceinline__ f16x8 buf_ld16(BufRsrc r, uint32_t byte_off) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
+    return __builtin_bit_cast(f16x8, v);
+}
+
 // Cross-lane exchange inside a wave64 (ds_bpermute based).
 __device__ __forceinline__ float xor_lane(float v, int mask) {
     return __shfl_xor(v, mask, kWave);

@@ -42,7 +42,6 @@ struct DecodeArgs {
     float* part_out;     // [Hq][nsplit][D]   (workspace)
     float* part_max;     // [Hq][nsplit]      (workspace, log2 domain)
     float* part_sum;     // [Hq][nsplit]      (workspace)
-    unsigned long long* counters;  // [Hkv] arrival counters inside part_sum's tail
     uint64_t kv_stride;
     uint32_t kv_len;     // patched per decode step
     uint32_t num_heads;
@@ -51,26 +50,27 @@ struct DecodeArgs {
     uint32_t head_dim;
     uint32_t nsplit;     // context splits per KV head (patched)
     uint32_t chunk;      // keys per split (patched)
-    uint32_t epoch;      // arrival-counter generation (patched)
     float scale_log2;    // log2(e) / sqrt(D)
-    uint32_t pad_;
 };
 
 struct DecodePlan {
-    int path;          // 0 = generic (any D, any stride), 1 = MFMA wave64 path (D = 128)
+    int path;          // 0 = generic (any D, any stride); 1/2/3 = MFMA split with 4/2/1 KV heads per workgroup + merge
     uint32_t nsplit;
     uint32_t chunk;
-    uint32_t block;    // threads per workgroup
+    uint32_t block;    // threads per split workgroup
 };
 
 DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_heads,
                        uint32_t head_dim, uint64_t kv_stride, const void* q, const void* k,
                        const void* v, int device);
-// Recompute split/chunk/counter fields of an existing argument struct for a
-// new kv_len (same path).  Used by launch and by the graph-node updater.
-void replan_decode(DecodeArgs& a, int path, int device);
-hipError_t launch_decode_kernel(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream);
-const void* decode_kernel_symbol(int path);
+// Recompute the split/chunk fields of an argument struct for its kv_len.
+// Used by launch and by the graph-node updaters (same plan for the same L).
+void replan_decode(DecodeArgs& a, int device);
+// Enqueues the split kernel and the merge kernel (two graph nodes).
+hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream);
+hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
+const void* decode_split_symbol(int path);
+const void* decode_merge_symbol();
 
 // ------------------------------------------------------------- prefill
 struct PrefillArgs {
@@ -119,7 +119,6 @@ enum Option {
     kOptDecodeForceGeneric = 0,
     kOptDecodeSplits = 1,        // 0 = automatic
     kOptPrefillForceGeneric = 2,
-    kOptDecodeWaves = 3,         // 0 = automatic
     kOptCount = 8
 };
 long get_option(int which);

@@ -25,6 +25,8 @@
 //    LDS buffers, one barrier per tile.
 #include "attn_internal.hpp"
 
+#include <type_traits>
+
 namespace attn {
 
 namespace {
@@ -64,13 +66,18 @@ __device__ __forceinline__ bool map_block(uint32_t bid, uint32_t quads, uint32_t
     return true;
 }
 
+// Lazy rescaling: the running maximum used for exp2 is only raised when a row
+// maximum exceeds it by more than kRescaleSlack (log2 units), so P <= 2^8 in
+// fp16 and the O^T accumulators are rarely touched by VALU code.
+constexpr float kRescaleSlack = 8.0f;
+
 __global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) f16 kt[2][kBN * kKP];
     __shared__ __attribute__((aligned(16))) f16 vt[2][kD * kVP];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: SGPR descriptors
     const int n = lane & 31;   // MFMA column (query) / A-operand row
     const int hh = lane >> 5;  // MFMA k-half / output row half
 
@@ -81,21 +88,22 @@ __global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
     const uint32_t g = (4u * quad) / a.group;
     const uint32_t N = a.seq_len;
     const uint32_t q0 = tile * kBM;
+    const uint32_t q_row_bytes = (uint32_t)(a.q_stride * 2);
+    const uint32_t kv_row_bytes = (uint32_t)(a.kv_stride * 2);
+
+    // buffer views: rows past N read as zero (no guards needed)
+    const BufRsrc rq = make_rsrc(a.q + (uint64_t)head * kD, (N - 1) * q_row_bytes + kD * 2);
+    const BufRsrc rk = make_rsrc(a.k + (uint64_t)g * kD, (N - 1) * kv_row_bytes + kD * 2);
+    const BufRsrc rv = make_rsrc(a.v + (uint64_t)g * kD, (N - 1) * kv_row_bytes + kD * 2);
 
     // Q^T B operands: lane (hh, n) of column tile nt holds
     // Q[q0 + 32nt + n][head][16s + 8hh .. +7] for k-step s.
     f16x8 qb[2][8];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-        const uint32_t row = q0 + 32u * nt + n;
-        if (row < N) {
-            const f16* p = a.q + (uint64_t)row * a.q_stride + (uint64_t)head * kD + 8 * hh;
+        const uint32_t off = (q0 + 32u * nt + n) * q_row_bytes + 16u * hh;
 #pragma unroll
-            for (int s = 0; s < 8; ++s) qb[nt][s] = ld16(p + 16 * s);
-        } else {
-#pragma unroll
-            for (int s = 0; s < 8; ++s) qb[nt][s] = f16x8{};
-        }
+        for (int s = 0; s < 8; ++s) qb[nt][s] = buf_ld16(rq, off + 32u * s);
     }
 
     f32x16 o[2][4];
@@ -103,12 +111,10 @@ __global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[nt][dt] = f32x16{};
-    float m_run[2] = {-INFINITY, -INFINITY};
+    float m_used[2] = {-INFINITY, -INFINITY};
     float l_run[2] = {0.f, 0.f};
 
     // global -> register staging of one 64-key tile
-    const f16* kbase = a.k + (uint64_t)g * kD;
-    const f16* vbase = a.v + (uint64_t)g * kD;
     const uint32_t kq = tid & 15;   // V: key quad (keys 4kq..4kq+3)
     const uint32_t dg = tid >> 4;   // V: dims 8dg..8dg+7
     f16x8 kr[4], vr[4];
@@ -116,14 +122,11 @@ __global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t e = (uint32_t)i * 256u + tid;
-            const uint32_t key = kv0 + (e >> 4);
-            kr[i] = key < N ? ld16(kbase + (uint64_t)key * a.kv_stride + 8u * (e & 15u)) : f16x8{};
+            kr[i] = buf_ld16(rk, (kv0 + (e >> 4)) * kv_row_bytes + 16u * (e & 15u));
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t key = kv0 + 4u * kq + r;
-            vr[r] = key < N ? ld16(vbase + (uint64_t)key * a.kv_stride + 8u * dg) : f16x8{};
-        }
+        for (int r = 0; r < 4; ++r)
+            vr[r] = buf_ld16(rv, (kv0 + 4u * kq + r) * kv_row_bytes + 16u * dg);
     };
     // key quad kq = 4ks + 2b + h lands in V^T slots ks*16 + h*8 + 4b .. +3,
     // the order in which S^T tile ks/2 presents keys to PV k-step ks.
@@ -145,16 +148,9 @@ __global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
         }
     };
 
-    const uint32_t n_tiles = tile + 1u;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-
-    for (uint32_t j = 0; j < n_tiles; ++j) {
-        const int buf = (int)(j & 1u);
-        if (j + 1 < n_tiles) gload((j + 1) * kBN);
-
-        // ---- S^T[key][query] = K . Q^T
+    // one 64-key tile: S^T = K . Q^T, online softmax, O^T += V^T . P^T
+    auto tile_step = [&](int buf, uint32_t j, auto diag_tag) {
+        constexpr bool kDiag = decltype(diag_tag)::value;
         f32x16 s[2][2];
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
@@ -169,46 +165,47 @@ __global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
                 for (int nt = 0; nt < 2; ++nt) s[nt][mt] = mfma32(ka, qb[nt][ks], s[nt][mt]);
             }
         }
-
-        // ---- online softmax (log2 domain), per lane = per query
-        const bool diag = (j == tile);
         f16x8 pb[2][4];
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            const uint32_t query = q0 + 32u * nt + n;
             float mx = -INFINITY;
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     float x = s[nt][mt][i];
-                    if (diag) {
+                    if constexpr (kDiag) {
+                        const uint32_t query = q0 + 32u * nt + n;
                         const uint32_t key = j * kBN + 32u * mt + 8u * (i >> 2) + 4u * hh + (i & 3);
                         if (key > query || key >= N) x = -INFINITY;
+                        s[nt][mt][i] = x;
                     }
-                    s[nt][mt][i] = x;
                     mx = fmaxf(mx, x);
                 }
             mx = fmaxf(mx, xor_lane(mx, 32));
-            const float m_new = fmaxf(m_run[nt], mx * a.scale_log2);
-            const float alpha = fast_exp2(m_run[nt] - m_new);
+            const float m_tile = mx * a.scale_log2;
+            const bool need = m_tile > m_used[nt] + kRescaleSlack;
+            if (__any(need)) {
+                const float m_new = need ? m_tile : m_used[nt];
+                const float alpha = fast_exp2(m_used[nt] - m_new);
+                l_run[nt] *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) o[nt][dt] *= alpha;
+                m_used[nt] = m_new;
+            }
+            const float mneg = -m_used[nt];
             float psum = 0.f;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
                 for (int r = 0; r < 8; ++r) {
-                    const float x = s[nt][ks >> 1][8 * (ks & 1) + r];
-                    const f16 p = (f16)fast_exp2(__builtin_fmaf(x, a.scale_log2, -m_new));
-                    pb[nt][ks][r] = p;
-                    psum += (float)p;
+                    const float p = fast_exp2(__builtin_fmaf(s[nt][ks >> 1][8 * (ks & 1) + r],
+                                                             a.scale_log2, mneg));
+                    pb[nt][ks][r] = (f16)p;
+                    psum += p;
                 }
-            l_run[nt] = l_run[nt] * alpha + psum;
-            m_run[nt] = m_new;
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt) o[nt][dt] *= alpha;
+            l_run[nt] += psum;
         }
-
-        // ---- O^T[dim][query] += V^T . P^T
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
@@ -218,10 +215,20 @@ __global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
                 for (int nt = 0; nt < 2; ++nt) o[nt][dt] = mfma32(va, pb[nt][ks], o[nt][dt]);
             }
         }
+    };
 
-        if (j + 1 < n_tiles) lstore(buf ^ 1);
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    // full tiles 0..tile-1 need no mask; tile `tile` holds the diagonal
+    for (uint32_t j = 0; j < tile; ++j) {
+        const int buf = (int)(j & 1u);
+        gload((j + 1) * kBN);
+        tile_step(buf, j, std::false_type{});
+        lstore(buf ^ 1);
         __syncthreads();
     }
+    tile_step((int)(tile & 1u), tile, std::true_type{});
 
     // ---- epilogue: O = O^T / l, packed [N][Hq][D]
 #pragma unroll
@@ -253,6 +260,9 @@ int plan_prefill(const PrefillArgs& a) {
     if (a.group == 0 || a.group % 4 != 0 || a.num_heads % 4 != 0) return 0;
     if (a.q_stride % 8 != 0 || a.kv_stride % 8 != 0) return 0;
     if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v) || !aligned16(a.out)) return 0;
+    // every row offset must fit the 32-bit buffer ranges
+    const uint64_t stride = a.q_stride > a.kv_stride ? a.q_stride : a.kv_stride;
+    if ((uint64_t)(a.seq_len + kBM) * stride * 2 + kD * 2 > 0xffffffffull) return 0;
     return 1;
 }
 

@@ -129,11 +129,11 @@ def test_decode_independent_of_split_plan(attn, gpu, splits):
     assert_close(got, e, 2e-3, 1e-2, f"splits={splits}")
 
 
-def test_decode_eight_wave_variant_and_generic(attn, gpu):
+def test_decode_forced_generic(attn, gpu):
     L = 5000
     q, k, v = smol_inputs(L, seed=10)
     e = expected(q, k, v, L)
-    for opt, val in (("decode_waves", 8), ("decode_force_generic", 1)):
+    for opt, val in (("decode_force_generic", 1),):
         attn.set_option(opt, val)
         try:
             print(f"[case] decode {opt}={val} plan={attn.decode_plan(L, 16, 4, 128)}", flush=True)
