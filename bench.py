@@ -319,7 +319,7 @@ def main():
     # ---- C4 prefill at 8192 tokens
     N = 8192
     pf_steps = max(5, min(50, steps // 4))
-    pms = bench_prefill(torch, A, N, pf_steps, 3)
+    pms = bench_prefill(torch, A, N, pf_steps, 20)  # warm-up lets the clock settle
     tflops = prefill_flops(N) / (pms * 1e-3) / 1e12
     log(f"prefill N={N}: {pms * 1e3:.1f} us  {tflops:.1f} TFLOP/s ({100 * tflops / PEAK_FP16_TFLOPS:.1f}% of fp16 peak)")
 

@@ -119,6 +119,7 @@ enum Option {
     kOptDecodeForceGeneric = 0,
     kOptDecodeSplits = 1,        // 0 = automatic
     kOptPrefillForceGeneric = 2,
+    kOptPrefillWaves = 3,        // 4 or 8 waves per workgroup (0 = 8)
     kOptCount = 8
 };
 long get_option(int which);

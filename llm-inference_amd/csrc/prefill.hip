@@ -6,9 +6,10 @@
 // position 0 and kv_len = N (:388-390).
 //
 // MFMA path (D = 128, Hq/Hkv a multiple of 4, 16-byte aligned rows):
-//  * workgroup = 4 waves = 4 query heads sharing one KV head, 64 query tokens.
-//    Every wave owns 64 queries of its head (two 32-column MFMA tiles) so each
-//    K/V operand fetched from LDS feeds two MFMAs.
+//  * workgroup = 64 query tokens of 4 query heads sharing one KV head, as 8
+//    waves (two per head, 32 queries each, 2 waves per SIMD so one wave's
+//    softmax overlaps the other's MFMAs; everything stays in VGPRs) or, as an
+//    option, 4 waves of 64 queries (each LDS operand feeds two MFMAs).
 //  * K and V of a 64-key tile are staged in LDS once per workgroup and shared
 //    by the 4 heads (the reference re-reads them per head).  V is stored
 //    transposed (V^T[dim][key]) with the keys of every 16-key MFMA step in the
@@ -71,7 +72,16 @@ __device__ __forceinline__ bool map_block(uint32_t bid, uint32_t quads, uint32_t
 // fp16 and the O^T accumulators are rarely touched by VALU code.
 constexpr float kRescaleSlack = 8.0f;
 
-__global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
+// NT 32-query column tiles per wave.  NT = 2: 4 waves (one per grouped head,
+// 64 queries each, 1 wave per SIMD); NT = 1: 8 waves (two per head, 32
+// queries each, 2 waves per SIMD so one wave's softmax overlaps the other's
+// MFMAs).  Either way a workgroup covers 64 query tokens of 4 heads.
+template <int NT>
+__global__ __launch_bounds__(256 * (2 / NT), 1) void prefill_d128(PrefillArgs a) {
+    constexpr int kWaves = 4 * (2 / NT);
+    constexpr int kThreads = 64 * kWaves;
+    constexpr int kKChunks = (kBN * kD / 8) / kThreads;  // 16 B K chunks per thread
+    constexpr int kVKeys = (kBN * kD / 8) / kThreads;    // V keys per thread (x 8 dims)
     __shared__ __attribute__((aligned(16))) f16 kt[2][kBN * kKP];
     __shared__ __attribute__((aligned(16))) f16 vt[2][kD * kVP];
 
@@ -84,10 +94,10 @@ __global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
     const uint32_t quads = a.num_heads / 4u;
     uint32_t quad, tile;
     if (!map_block(blockIdx.x, quads, a.q_tiles, quad, tile)) return;
-    const uint32_t head = 4u * quad + (uint32_t)wave;
+    const uint32_t head = 4u * quad + (uint32_t)(wave & 3);
     const uint32_t g = (4u * quad) / a.group;
     const uint32_t N = a.seq_len;
-    const uint32_t q0 = tile * kBM;
+    const uint32_t q0 = tile * kBM + 32u * NT * (uint32_t)(wave >> 2);  // this wave's first query
     const uint32_t q_row_bytes = (uint32_t)(a.q_stride * 2);
     const uint32_t kv_row_bytes = (uint32_t)(a.kv_stride * 2);
 
@@ -98,76 +108,99 @@ __global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
 
     // Q^T B operands: lane (hh, n) of column tile nt holds
     // Q[q0 + 32nt + n][head][16s + 8hh .. +7] for k-step s.
-    f16x8 qb[2][8];
+    f16x8 qb[NT][8];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
         const uint32_t off = (q0 + 32u * nt + n) * q_row_bytes + 16u * hh;
 #pragma unroll
         for (int s = 0; s < 8; ++s) qb[nt][s] = buf_ld16(rq, off + 32u * s);
     }
 
-    f32x16 o[2][4];
+    f32x16 o[NT][4];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[nt][dt] = f32x16{};
-    float m_used[2] = {-INFINITY, -INFINITY};
-    float l_run[2] = {0.f, 0.f};
+    float m_used[NT], l_run[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        m_used[nt] = -INFINITY;
+        l_run[nt] = 0.f;
+    }
 
-    // global -> register staging of one 64-key tile
-    const uint32_t kq = tid & 15;   // V: key quad (keys 4kq..4kq+3)
-    const uint32_t dg = tid >> 4;   // V: dims 8dg..8dg+7
-    f16x8 kr[4], vr[4];
+    // global -> register staging of one 64-key tile: K as 16 B chunks, V as
+    // kVKeys consecutive keys x 8 dims per thread (transposed on the LDS store)
+    constexpr uint32_t kKeyGroups = kBN / kVKeys;
+    const uint32_t kgrp = tid % kKeyGroups;  // keys kVKeys*kgrp ..
+    const uint32_t dg = tid / kKeyGroups;    // dims 8dg..8dg+7
+    f16x8 kr[kKChunks], vr[kVKeys];
     auto gload = [&](uint32_t kv0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t e = (uint32_t)i * 256u + tid;
+        for (int i = 0; i < kKChunks; ++i) {
+            const uint32_t e = (uint32_t)i * kThreads + tid;
             kr[i] = buf_ld16(rk, (kv0 + (e >> 4)) * kv_row_bytes + 16u * (e & 15u));
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            vr[r] = buf_ld16(rv, (kv0 + 4u * kq + r) * kv_row_bytes + 16u * dg);
+        for (int r = 0; r < kVKeys; ++r)
+            vr[r] = buf_ld16(rv, (kv0 + kVKeys * kgrp + r) * kv_row_bytes + 16u * dg);
     };
-    // key quad kq = 4ks + 2b + h lands in V^T slots ks*16 + h*8 + 4b .. +3,
-    // the order in which S^T tile ks/2 presents keys to PV k-step ks.
-    const uint32_t vslot = (kq >> 2) * 16u + (kq & 1u) * 8u + ((kq >> 1) & 1u) * 4u;
+    // key 16ks + 8b + 4h + r sits in V^T slot ks*16 + h*8 + 4b + r: the order
+    // in which S^T tile ks/2 presents keys to PV k-step ks
+    const uint32_t key0 = kVKeys * kgrp;
+    const uint32_t vslot = (key0 >> 4) * 16u + ((key0 >> 2) & 1u) * 8u + ((key0 >> 3) & 1u) * 4u +
+                           (key0 & 3u);
     auto lstore = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t e = (uint32_t)i * 256u + tid;
+        for (int i = 0; i < kKChunks; ++i) {
+            const uint32_t e = (uint32_t)i * kThreads + tid;
             *reinterpret_cast<f16x8*>(&kt[buf][(e >> 4) * kKP + 8u * (e & 15u)]) = kr[i];
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            f16x4 w;
-            w[0] = vr[0][j];
-            w[1] = vr[1][j];
-            w[2] = vr[2][j];
-            w[3] = vr[3][j];
-            *reinterpret_cast<f16x4*>(&vt[buf][(8u * dg + j) * kVP + vslot]) = w;
+            if constexpr (kVKeys == 4) {
+                f16x4 w;
+                w[0] = vr[0][j];
+                w[1] = vr[1][j];
+                w[2] = vr[2][j];
+                w[3] = vr[3][j];
+                *reinterpret_cast<f16x4*>(&vt[buf][(8u * dg + j) * kVP + vslot]) = w;
+            } else {
+                f16x2 w;
+                w[0] = vr[0][j];
+                w[1] = vr[1][j];
+                *reinterpret_cast<f16x2*>(&vt[buf][(8u * dg + j) * kVP + vslot]) = w;
+            }
         }
     };
 
     // one 64-key tile: S^T = K . Q^T, online softmax, O^T += V^T . P^T
     auto tile_step = [&](int buf, uint32_t j, auto diag_tag) {
         constexpr bool kDiag = decltype(diag_tag)::value;
-        f32x16 s[2][2];
+        f32x16 s[NT][2];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) s[nt][mt] = f32x16{};
+        // K operands are read one k-step ahead of their MFMAs
+        const f16* kbuf = &kt[buf][n * kKP + 8 * hh];
+        f16x8 ka[2][2];
+        ka[0][0] = lds16(kbuf);
+        ka[0][1] = lds16(kbuf + 32 * kKP);
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                const f16x8 ka = lds16(&kt[buf][(32 * mt + n) * kKP + 16 * ks + 8 * hh]);
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) s[nt][mt] = mfma32(ka, qb[nt][ks], s[nt][mt]);
+            const int cur = ks & 1;
+            if (ks + 1 < 8) {
+                ka[cur ^ 1][0] = lds16(kbuf + 16 * (ks + 1));
+                ka[cur ^ 1][1] = lds16(kbuf + 32 * kKP + 16 * (ks + 1));
             }
-        }
-        f16x8 pb[2][4];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) s[nt][mt] = mfma32(ka[cur][mt], qb[nt][ks], s[nt][mt]);
+        }
+        float m_tile[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
             float mx = -INFINITY;
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt)
@@ -183,38 +216,64 @@ __global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
                     mx = fmaxf(mx, x);
                 }
             mx = fmaxf(mx, xor_lane(mx, 32));
-            const float m_tile = mx * a.scale_log2;
-            const bool need = m_tile > m_used[nt] + kRescaleSlack;
-            if (__any(need)) {
-                const float m_new = need ? m_tile : m_used[nt];
-                const float alpha = fast_exp2(m_used[nt] - m_new);
-                l_run[nt] *= alpha;
+            m_tile[nt] = mx * a.scale_log2;
+        }
+        // one (rarely taken) block rescales every column tile, so no part of
+        // it is speculated into the common path
+        bool need[NT];
+        bool any = false;
 #pragma unroll
-                for (int dt = 0; dt < 4; ++dt) o[nt][dt] *= alpha;
-                m_used[nt] = m_new;
+        for (int nt = 0; nt < NT; ++nt) {
+            need[nt] = m_tile[nt] > m_used[nt] + kRescaleSlack;
+            any = any || need[nt];
+        }
+        if (__any(any)) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const float mn = need[nt] ? m_tile[nt] : m_used[nt];
+                const float al = fast_exp2(m_used[nt] - mn);
+                l_run[nt] *= al;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) o[nt][dt] *= al;
+                m_used[nt] = mn;
             }
-            const float mneg = -m_used[nt];
-            float psum = 0.f;
+        }
+        float mneg[NT], psum[NT];
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
+        for (int nt = 0; nt < NT; ++nt) {
+            mneg[nt] = -m_used[nt];
+            psum[nt] = 0.f;
+        }
+        // P one 16-key MFMA step at a time, consumed at once by that step's
+        // PV MFMAs: exps of step ks+1 overlap the MFMAs of step ks
+        const f16* vbuf = &vt[buf][n * kVP + 8 * hh];
 #pragma unroll
-                for (int r = 0; r < 8; ++r) {
-                    const float p = fast_exp2(__builtin_fmaf(s[nt][ks >> 1][8 * (ks & 1) + r],
-                                                             a.scale_log2, mneg));
-                    pb[nt][ks][r] = (f16)p;
-                    psum += p;
+        for (int ks = 0; ks < 4; ++ks) {
+            f16x8 va[4];
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) va[dt] = lds16(vbuf + 32 * dt * kVP + 16 * ks);
+            f16x8 pb[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+                    pb[nt][r] = (f16)fast_exp2(__builtin_fmaf(s[nt][ks >> 1][8 * (ks & 1) + r],
+                                                              a.scale_log2, mneg[nt]));
+                // row sum of the fp16 weights the PV product uses, two per
+                // v_dot2_f32_f16 (fp32 accumulate)
+#pragma unroll
+                for (int r = 0; r < 8; r += 2) {
+                    const f16x2 pair = {pb[nt][r], pb[nt][r + 1]};
+                    psum[nt] = __builtin_amdgcn_fdot2(pair, f16x2{(f16)1.0f, (f16)1.0f}, psum[nt], false);
                 }
-            l_run[nt] += psum;
-        }
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const f16x8 va = lds16(&vt[buf][(32 * dt + n) * kVP + 16 * ks + 8 * hh]);
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) o[nt][dt] = mfma32(va, pb[nt][ks], o[nt][dt]);
             }
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) o[nt][dt] = mfma32(va[dt], pb[nt], o[nt][dt]);
         }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) l_run[nt] += psum[nt];
     };
 
     gload(0);
@@ -232,7 +291,7 @@ __global__ __launch_bounds__(256, 1) void prefill_d128(PrefillArgs a) {
 
     // ---- epilogue: O = O^T / l, packed [N][Hq][D]
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
         const float l = l_run[nt] + xor_lane(l_run[nt], 32);
         const float inv = 1.f / l;
         const uint32_t query = q0 + 32u * nt + n;
@@ -277,7 +336,11 @@ hipError_t launch_prefill_kernel(const PrefillArgs& a, int path, hipStream_t str
         blocks = (uint64_t)a.q_tiles * quads;
     }
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(prefill_d128, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+    if (get_option(kOptPrefillWaves) == 4) {
+        hipLaunchKernelGGL(prefill_d128<2>, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(prefill_d128<1>, dim3((uint32_t)blocks), dim3(512), 0, stream, a);
+    }
     return hipGetLastError();
 }
 
