@@ -1,0 +1,131 @@
+// Attention hot-path launch API, declared exactly as in the reference's
+// include/kernels/kernels.hpp (same names, parameter types, order and default
+// arguments), so ModelInference (model_inference.hpp) and the reference tests
+// compile unchanged against it.  Definitions live in
+// llm-inference_amd/csrc/kernels_api.cpp (libattn_mi355x.so) and forward to the
+// C ABI in include/attn_mi355x.h.  Only the attention subset is declared here;
+// the GEMM/GEMV/norm/embedding launchers of the reference are outside this
+// library.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <cstdint>
+#include <cstddef>
+#include <hip/hip_runtime.h>
+
+// kernels.hpp:47-59
+void launch_rope(
+    __half* d_q,                 // [seq_len, num_heads, head_dim]
+    __half* d_k,                 // [seq_len, num_kv_heads, head_dim]
+    const __half* d_cos,         // [max_seq_len, head_dim / 2]
+    const __half* d_sin,         // [max_seq_len, head_dim / 2]
+    size_t seq_len,
+    size_t num_heads,
+    size_t num_kv_heads,
+    size_t head_dim,
+    size_t q_stride,
+    size_t k_stride,
+    size_t start_pos = 0         // Position offset (0 for prefill)
+);
+
+// kernels.hpp:62-79
+void launch_rope_and_store_kv(
+    __half* d_q,                 // [seq_len, num_heads, head_dim]
+    __half* d_k,                 // [seq_len, num_kv_heads, head_dim]
+    __half* d_v,                 // [seq_len, num_kv_heads, head_dim]
+    __half* d_k_cache,           // [max_seq_len, num_kv_heads, head_dim]
+    __half* d_v_cache,           // [max_seq_len, num_kv_heads, head_dim]
+    const __half* d_cos,         // [max_seq_len, head_dim / 2]
+    const __half* d_sin,         // [max_seq_len, head_dim / 2]
+    size_t seq_len,
+    size_t num_heads,
+    size_t num_kv_heads,
+    size_t head_dim,
+    size_t q_stride,
+    size_t k_stride,
+    size_t start_pos,            // Position offset (0 for prefill)
+    bool apply_rotation,
+    hipStream_t stream = nullptr
+);
+
+// kernels.hpp:81-86
+void update_rope_and_store_kv_node(
+    hipGraphExec_t graph_exec,
+    hipGraphNode_t node,
+    size_t start_pos,
+    bool apply_rotation
+);
+
+// kernels.hpp:88-99 (launched on the null stream, as in the reference)
+void launch_causal_attention_prefill(
+    const __half* d_q,
+    const __half* d_k,
+    const __half* d_v,
+    __half* d_out,
+    size_t seq_len,
+    size_t num_heads,
+    size_t num_kv_heads,
+    size_t head_dim,
+    size_t q_stride = 0,  // Elements between tokens; 0 means packed Q.
+    size_t kv_stride = 0  // Elements between tokens; 0 means packed K/V.
+);
+
+// kernels.hpp:103: workspace sizing unit (tokens per partial state)
+#define KV_CHUNK 12
+
+// kernels.hpp:104-123
+void launch_causal_attention_decode(
+    const __half* d_q,              // [1, num_heads, head_dim]
+    const __half* d_k_cache,        // [kv_cache_len, num_kv_heads, head_dim]
+    const __half* d_v_cache,        // [kv_cache_len, num_kv_heads, head_dim]
+    __half* d_out,                  // [1, num_heads, head_dim]
+    float* d_partial_out,           // [num_heads, num_kv_chunks, head_dim]
+    float* d_partial_max,           // [num_heads, num_kv_chunks]
+    float* d_partial_weight_sum,    // [num_heads, num_kv_chunks]
+    size_t query_len,               // Must be 1 for this decode implementation.
+    size_t kv_cache_len,            // Number of valid cached tokens.
+    size_t start_pos,               // Absolute position of the query token.
+    size_t num_heads,
+    size_t num_kv_heads,
+    size_t head_dim,
+    size_t q_stride,                // Elements between Q tokens; 0 means packed.
+    size_t kv_stride,               // Elements between K/V tokens; 0 means packed.
+    hipStream_t stream = nullptr,
+    hipGraphNode_t* attention_node = nullptr,
+    hipGraphNode_t* merge_node = nullptr
+);
+
+// kernels.hpp:127-146
+void launch_causal_attention_decode_vectorized(
+    const __half* d_q,
+    const __half* d_k_cache,
+    const __half* d_v_cache,
+    __half* d_out,
+    float* d_partial_out,
+    float* d_partial_max,
+    float* d_partial_weight_sum,
+    size_t query_len,
+    size_t kv_cache_len,
+    size_t start_pos,
+    size_t num_heads,
+    size_t num_kv_heads,
+    size_t head_dim,
+    size_t q_stride = 0,
+    size_t kv_stride = 0,
+    hipStream_t stream = nullptr,
+    hipGraphNode_t* attention_node = nullptr,
+    hipGraphNode_t* merge_node = nullptr
+);
+
+// kernels.hpp:148-152
+void update_merge_attention_decode_node(
+    hipGraphExec_t graph_exec,
+    hipGraphNode_t node,
+    size_t kv_cache_len
+);
+
+// kernels.hpp:190-194
+void update_causal_attention_decode_node(
+    hipGraphExec_t graph_exec,
+    hipGraphNode_t node,
+    size_t kv_cache_len
+);

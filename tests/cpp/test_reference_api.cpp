@@ -1,0 +1,427 @@
+// Exercises libattn_mi355x.so through the reference's own C++ interface
+// (include/kernels/kernels.hpp, kv_cache.hpp, rope_cache.hpp, gpu_utils.hpp),
+// the way the reference's tests and ModelInference use it:
+//   1. Flash-Decode known-answer test, tests/test_causal_attention.cpp:152-228
+//      (closed-form inputs, fp64 CPU softmax, output guards, 2e-3/2e-3).
+//   2. RoPE + KV cache append, tests/test_rope.cpp:92-195 (interleaved/packed x
+//      rotate/NoPE x start_pos {0, 2}; sentinel rows; other layer and sources
+//      untouched; NoPE and V bit-exact), on seeded synthetic inputs.
+//   3. Decode at every position vs the prefill row, test_causal_attention.cpp:80-150
+//      (cache rows past L hold 123, output guards -123, interleaved Q stride).
+//   4. A graph-captured decode step over several layers with per-step node
+//      patching, model_inference.hpp:96-134, compared with eager launches.
+// Prints one PASS/FAIL line per test; exit status is the number of failures.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <vector>
+
+#include "../../include/gpu_utils.hpp"
+#include "../../include/kernels/kernels.hpp"
+#include "../../include/kv_cache.hpp"
+#include "../../include/rope_cache.hpp"
+
+namespace {
+
+struct Config {
+    size_t num_layers, max_seq_len, num_kv_heads, head_dim;
+};
+
+int g_failures = 0;
+
+void report(const char* name, bool ok, const char* detail = "") {
+    std::printf("%s %s %s\n", ok ? "PASS" : "FAIL", name, detail);
+    std::fflush(stdout);
+    if (!ok) ++g_failures;
+}
+
+template <typename T>
+T* upload(const std::vector<T>& h) {
+    T* d = nullptr;
+    HIP_CHECK(hipMalloc(&d, h.size() * sizeof(T)));
+    HIP_CHECK(hipMemcpy(d, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice));
+    return d;
+}
+
+template <typename T>
+std::vector<T> download(const T* d, size_t n) {
+    std::vector<T> h(n);
+    HIP_CHECK(hipMemcpy(h.data(), d, n * sizeof(T), hipMemcpyDeviceToHost));
+    return h;
+}
+
+bool close(const __half* a, const __half* e, size_t n, float atol, float rtol, float* maxd) {
+    bool ok = true;
+    *maxd = 0.f;
+    for (size_t i = 0; i < n; ++i) {
+        const float x = __half2float(a[i]), y = __half2float(e[i]);
+        const float d = std::fabs(x - y);
+        *maxd = std::max(*maxd, d);
+        if (!(d <= atol + rtol * std::fabs(y)) || !std::isfinite(x)) ok = false;
+    }
+    return ok;
+}
+
+bool same_bits(const __half* a, const __half* b, size_t n) {
+    return std::memcmp(a, b, n * sizeof(__half)) == 0;
+}
+
+// ---------------------------------------------------------------- test 1
+void test_flash_decode_kat() {
+    const size_t lengths[] = {1, KV_CHUNK, KV_CHUNK + 1, 3 * KV_CHUNK + 1, 257};
+    bool all = true;
+    float worst = 0.f;
+    for (size_t head_dim : {size_t(32), size_t(128)})
+        for (size_t kv_heads : {size_t(1), size_t(2), size_t(4)})
+            for (size_t len : lengths)
+                for (bool padded : {false, true}) {
+                    const size_t heads = 4, q_dim = heads * head_dim, kv_dim = kv_heads * head_dim;
+                    const size_t stride = kv_dim + (padded ? 17 : 0);
+                    std::vector<__half> q(q_dim), k((len + 2) * stride, __float2half(123.f));
+                    auto v = k;
+                    for (size_t i = 0; i < q.size(); ++i)
+                        q[i] = __float2half(2.f * std::sin(float(i + 1) * .37f));
+                    for (size_t t = 0; t < len; ++t)
+                        for (size_t i = 0; i < kv_dim; ++i) {
+                            k[t * stride + i] = __float2half(3.f * std::cos(float(t * kv_dim + i + 1) * .13f));
+                            v[t * stride + i] = __float2half(std::sin(float(t * kv_dim + i + 3) * .19f));
+                        }
+                    std::vector<__half> expected(q_dim);
+                    for (size_t hd = 0; hd < heads; ++hd) {
+                        const size_t kh = hd / (heads / kv_heads);
+                        std::vector<double> sc(len);
+                        double mx = -INFINITY, den = 0.;
+                        for (size_t t = 0; t < len; ++t) {
+                            double dot = 0.;
+                            for (size_t c = 0; c < head_dim; ++c)
+                                dot += double(__half2float(q[hd * head_dim + c])) *
+                                       __half2float(k[t * stride + kh * head_dim + c]);
+                            sc[t] = dot / std::sqrt(double(head_dim));
+                            mx = std::max(mx, sc[t]);
+                        }
+                        for (auto& x : sc) {
+                            x = std::exp(x - mx);
+                            den += x;
+                        }
+                        for (size_t c = 0; c < head_dim; ++c) {
+                            double num = 0.;
+                            for (size_t t = 0; t < len; ++t)
+                                num += sc[t] * __half2float(v[t * stride + kh * head_dim + c]);
+                            expected[hd * head_dim + c] = __float2half(float(num / den));
+                        }
+                    }
+                    const size_t states = heads * ((len + KV_CHUNK - 1) / KV_CHUNK);
+                    __half *dq = upload(q), *dk = upload(k), *dv = upload(v);
+                    std::vector<__half> actual(q_dim + 2, __float2half(-123.f));
+                    __half* out = upload(actual);
+                    float *partial, *maximum, *sum;
+                    HIP_CHECK(hipMalloc(&partial, states * head_dim * sizeof(float)));
+                    HIP_CHECK(hipMalloc(&maximum, states * sizeof(float)));
+                    HIP_CHECK(hipMalloc(&sum, states * sizeof(float)));
+                    launch_causal_attention_decode(dq, dk, dv, out + 1, partial, maximum, sum, 1,
+                                                   len, len - 1, heads, kv_heads, head_dim, 0,
+                                                   padded ? stride : 0);
+                    HIP_CHECK(hipGetLastError());
+                    HIP_CHECK(hipDeviceSynchronize());
+                    actual = download(out, q_dim + 2);
+                    float md = 0.f;
+                    const bool ok = close(actual.data() + 1, expected.data(), q_dim, 2e-3f, 2e-3f, &md) &&
+                                    __half2float(actual.front()) == -123.f &&
+                                    __half2float(actual.back()) == -123.f;
+                    worst = std::max(worst, md);
+                    if (!ok) {
+                        std::printf("  KAT mismatch: D=%zu kv=%zu len=%zu padded=%d max|d|=%g\n",
+                                    head_dim, kv_heads, len, (int)padded, md);
+                        all = false;
+                    }
+                    for (void* p : {(void*)dq, (void*)dk, (void*)dv, (void*)out, (void*)partial,
+                                    (void*)maximum, (void*)sum})
+                        HIP_CHECK(hipFree(p));
+                }
+    char detail[64];
+    std::snprintf(detail, sizeof detail, "(max |diff| %.2e)", worst);
+    report("flash_decode_vs_cpu_softmax_kat", all, detail);
+}
+
+// CPU rotate-half with fp32 products rounded separately (rope.hip.cpp:53-57)
+void cpu_rotate(__half* x, const __half* c, const __half* s, size_t half) {
+    for (size_t i = 0; i < half; ++i) {
+        const float x0 = __half2float(x[i]), x1 = __half2float(x[i + half]);
+        const float cc = __half2float(c[i]), ss = __half2float(s[i]);
+        volatile float p0 = x0 * cc, p1 = x1 * ss, p2 = x1 * cc, p3 = x0 * ss;
+        x[i] = __float2half(p0 - p1);
+        x[i + half] = __float2half(p2 + p3);
+    }
+}
+
+// ---------------------------------------------------------------- test 2
+void test_rope_and_store_kv() {
+    const size_t heads = 16, kv_heads = 4, head_dim = 128, seq_len = 37;
+    const size_t q_dim = heads * head_dim, kv_dim = kv_heads * head_dim;
+    const size_t total_dim = q_dim + 2 * kv_dim;
+    Config cfg{2, seq_len + 2, kv_heads, head_dim};
+    KVCache cache(cfg);
+    RopeCache rope = create_rope_cache(cfg.max_seq_len, head_dim, 5.0e6f);
+    const auto cos_h = download(rope.d_cos, cfg.max_seq_len * head_dim / 2);
+    const auto sin_h = download(rope.d_sin, cfg.max_seq_len * head_dim / 2);
+    std::mt19937 gen(7);
+    std::normal_distribution<float> nd;
+    std::vector<__half> in_q(seq_len * q_dim), in_k(seq_len * kv_dim), in_v(seq_len * kv_dim);
+    for (auto* vec : {&in_q, &in_k, &in_v})
+        for (auto& x : *vec) x = __float2half(nd(gen));
+    const size_t cache_elements = cfg.max_seq_len * kv_dim;
+    const std::vector<__half> sentinel(cache_elements, __float2half(-123.f));
+    bool all = true;
+    for (bool interleaved : {false, true})
+        for (bool rotate : {false, true})
+            for (size_t start_pos : {size_t(0), size_t(2)}) {
+                const size_t count = seq_len - start_pos;
+                std::vector<__half> source;
+                size_t q_off = 0, k_off, v_off, q_stride, kv_stride;
+                if (interleaved) {
+                    source.resize(count * total_dim);
+                    k_off = q_dim;
+                    v_off = q_dim + kv_dim;
+                    q_stride = kv_stride = total_dim;
+                    for (size_t t = 0; t < count; ++t) {
+                        std::copy_n(in_q.data() + (start_pos + t) * q_dim, q_dim, source.data() + t * total_dim);
+                        std::copy_n(in_k.data() + (start_pos + t) * kv_dim, kv_dim, source.data() + t * total_dim + k_off);
+                        std::copy_n(in_v.data() + (start_pos + t) * kv_dim, kv_dim, source.data() + t * total_dim + v_off);
+                    }
+                } else {
+                    source.insert(source.end(), in_q.begin() + start_pos * q_dim, in_q.end());
+                    k_off = source.size();
+                    source.insert(source.end(), in_k.begin() + start_pos * kv_dim, in_k.end());
+                    v_off = source.size();
+                    source.insert(source.end(), in_v.begin() + start_pos * kv_dim, in_v.end());
+                    q_stride = q_dim;
+                    kv_stride = kv_dim;
+                }
+                const auto original = source;
+                __half* d_source = upload(source);
+                for (size_t layer = 0; layer < cfg.num_layers; ++layer) {
+                    HIP_CHECK(hipMemcpy(cache.get_k_cache(layer), sentinel.data(), cache_elements * 2, hipMemcpyHostToDevice));
+                    HIP_CHECK(hipMemcpy(cache.get_v_cache(layer), sentinel.data(), cache_elements * 2, hipMemcpyHostToDevice));
+                }
+                launch_rope_and_store_kv(d_source + q_off, d_source + k_off, d_source + v_off,
+                                         cache.get_k_cache(1), cache.get_v_cache(1), rope.d_cos,
+                                         rope.d_sin, count, heads, kv_heads, head_dim, q_stride,
+                                         kv_stride, start_pos, rotate);
+                HIP_CHECK(hipGetLastError());
+                HIP_CHECK(hipDeviceSynchronize());
+                // expected K/V cache rows and Q
+                auto exp_k = sentinel, exp_v = sentinel;
+                std::vector<__half> exp_q(count * q_dim);
+                for (size_t t = 0; t < count; ++t) {
+                    const size_t pos = start_pos + t;
+                    std::copy_n(in_k.data() + pos * kv_dim, kv_dim, exp_k.data() + pos * kv_dim);
+                    std::copy_n(in_v.data() + pos * kv_dim, kv_dim, exp_v.data() + pos * kv_dim);
+                    std::copy_n(in_q.data() + pos * q_dim, q_dim, exp_q.data() + t * q_dim);
+                    if (rotate) {
+                        for (size_t hd = 0; hd < kv_heads; ++hd)
+                            cpu_rotate(exp_k.data() + pos * kv_dim + hd * head_dim,
+                                       cos_h.data() + pos * head_dim / 2,
+                                       sin_h.data() + pos * head_dim / 2, head_dim / 2);
+                        for (size_t hd = 0; hd < heads; ++hd)
+                            cpu_rotate(exp_q.data() + t * q_dim + hd * head_dim,
+                                       cos_h.data() + pos * head_dim / 2,
+                                       sin_h.data() + pos * head_dim / 2, head_dim / 2);
+                    }
+                }
+                const auto act_k = download(cache.get_k_cache(1), cache_elements);
+                const auto act_v = download(cache.get_v_cache(1), cache_elements);
+                const auto act_src = download(d_source, source.size());
+                bool ok = same_bits(act_k.data(), exp_k.data(), cache_elements) &&
+                          same_bits(act_v.data(), exp_v.data(), cache_elements);
+                for (const __half* p : {cache.get_k_cache(0), cache.get_v_cache(0)}) {
+                    const auto untouched = download(p, cache_elements);
+                    ok = ok && same_bits(untouched.data(), sentinel.data(), cache_elements);
+                }
+                for (size_t t = 0; t < count; ++t) {
+                    ok = ok && same_bits(act_src.data() + q_off + t * q_stride, exp_q.data() + t * q_dim, q_dim);
+                    ok = ok && same_bits(act_src.data() + k_off + t * kv_stride, original.data() + k_off + t * kv_stride, kv_dim);
+                    ok = ok && same_bits(act_src.data() + v_off + t * kv_stride, original.data() + v_off + t * kv_stride, kv_dim);
+                }
+                if (!ok) {
+                    std::printf("  rope mismatch: interleaved=%d rotate=%d start=%zu\n", (int)interleaved, (int)rotate, start_pos);
+                    all = false;
+                }
+                HIP_CHECK(hipFree(d_source));
+            }
+    report("rope_and_store_kv_bitexact", all);
+}
+
+// ---------------------------------------------------------------- test 3
+void test_decode_vs_prefill_rows() {
+    const size_t heads = 16, kv_heads = 4, head_dim = 128, seq_len = 70;
+    const size_t q_dim = heads * head_dim, kv_dim = kv_heads * head_dim;
+    Config cfg{1, seq_len + 2, kv_heads, head_dim};
+    KVCache cache(cfg);
+    std::mt19937 gen(11);
+    std::normal_distribution<float> nd;
+    std::vector<__half> q(seq_len * q_dim);
+    std::vector<__half> ck(cfg.max_seq_len * kv_dim, __float2half(123.f)), cv = ck;
+    for (auto& x : q) x = __float2half(nd(gen));
+    for (size_t i = 0; i < seq_len * kv_dim; ++i) {
+        ck[i] = __float2half(nd(gen));
+        cv[i] = __float2half(nd(gen));
+    }
+    HIP_CHECK(hipMemcpy(cache.get_k_cache(0), ck.data(), ck.size() * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(cache.get_v_cache(0), cv.data(), cv.size() * 2, hipMemcpyHostToDevice));
+    __half* dq = upload(q);
+    __half* dpre;
+    HIP_CHECK(hipMalloc(&dpre, q.size() * 2));
+    launch_causal_attention_prefill(dq, cache.get_k_cache(0), cache.get_v_cache(0), dpre, seq_len,
+                                    heads, kv_heads, head_dim, q_dim, kv_dim);
+    HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipDeviceSynchronize());
+    const auto pre = download(dpre, q.size());
+    bool all = true;
+    float worst = 0.f;
+    for (bool interleaved : {false, true})
+        for (size_t pos = 0; pos < seq_len; ++pos) {
+            const size_t stride = interleaved ? q_dim + 2 * kv_dim : q_dim;
+            std::vector<__half> input(stride, __float2half(-123.f));
+            std::copy_n(q.data() + pos * q_dim, q_dim, input.data());
+            __half* d_in = upload(input);
+            std::vector<__half> output(3 * q_dim, __float2half(-123.f));
+            const auto guards = output;
+            __half* d_out = upload(output);
+            const size_t states = heads * ((pos + 1 + KV_CHUNK - 1) / KV_CHUNK);
+            float *po, *pm, *ps;
+            HIP_CHECK(hipMalloc(&po, states * head_dim * 4));
+            HIP_CHECK(hipMalloc(&pm, states * 4));
+            HIP_CHECK(hipMalloc(&ps, states * 4));
+            launch_causal_attention_decode_vectorized(d_in, cache.get_k_cache(0), cache.get_v_cache(0),
+                                                      d_out + q_dim, po, pm, ps, 1, pos + 1, pos,
+                                                      heads, kv_heads, head_dim,
+                                                      interleaved ? stride : 0, 0);
+            HIP_CHECK(hipGetLastError());
+            HIP_CHECK(hipDeviceSynchronize());
+            output = download(d_out, 3 * q_dim);
+            float md = 0.f;
+            const bool ok = close(output.data() + q_dim, pre.data() + pos * q_dim, q_dim, 4e-3f, 1e-2f, &md) &&
+                            same_bits(output.data(), guards.data(), q_dim) &&
+                            same_bits(output.data() + 2 * q_dim, guards.data(), q_dim);
+            worst = std::max(worst, md);
+            if (!ok) {
+                std::printf("  decode/prefill mismatch at pos %zu interleaved %d (max %g)\n", pos, (int)interleaved, md);
+                all = false;
+            }
+            for (void* p : {(void*)d_in, (void*)d_out, (void*)po, (void*)pm, (void*)ps}) HIP_CHECK(hipFree(p));
+        }
+    HIP_CHECK(hipFree(dq));
+    HIP_CHECK(hipFree(dpre));
+    char detail[64];
+    std::snprintf(detail, sizeof detail, "(max |diff| %.2e)", worst);
+    report("decode_vs_prefill_rows", all, detail);
+}
+
+// ---------------------------------------------------------------- test 4
+// model_inference.hpp:96-134: capture the decode step once (per layer: RoPE +
+// KV append, then Flash-Decode), then per token patch the three nodes of every
+// layer and replay.  Each replay must equal eager launches of the same step.
+void test_graph_decode_step() {
+    const size_t layers = 4, heads = 16, kv_heads = 4, head_dim = 128;
+    const size_t q_dim = heads * head_dim, kv_dim = kv_heads * head_dim, total = q_dim + 2 * kv_dim;
+    const size_t prompt = 300, steps = 5;
+    Config cfg{layers, prompt + steps + 1, kv_heads, head_dim};
+    KVCache graph_cache(cfg), eager_cache(cfg);
+    RopeCache rope = create_rope_cache(cfg.max_seq_len, head_dim, 5.0e6f);
+    std::mt19937 gen(3);
+    std::normal_distribution<float> nd;
+    std::vector<__half> cache_init(cfg.num_layers * 2 * cfg.max_seq_len * kv_dim);
+    for (auto& x : cache_init) x = __float2half(nd(gen));
+    HIP_CHECK(hipMemcpy(graph_cache.get_k_cache(0), cache_init.data(), cache_init.size() * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(eager_cache.get_k_cache(0), cache_init.data(), cache_init.size() * 2, hipMemcpyHostToDevice));
+    std::vector<std::vector<__half>> qkv_steps(steps, std::vector<__half>(layers * total));
+    for (auto& st : qkv_steps)
+        for (auto& x : st) x = __float2half(nd(gen));
+    __half *d_qkv_g, *d_qkv_e, *d_out_g, *d_out_e;
+    HIP_CHECK(hipMalloc(&d_qkv_g, layers * total * 2));
+    HIP_CHECK(hipMalloc(&d_qkv_e, layers * total * 2));
+    HIP_CHECK(hipMalloc(&d_out_g, layers * q_dim * 2));
+    HIP_CHECK(hipMalloc(&d_out_e, layers * q_dim * 2));
+    const size_t cap = heads * ((cfg.max_seq_len + KV_CHUNK - 1) / KV_CHUNK);
+    float *po, *pm, *ps;
+    HIP_CHECK(hipMalloc(&po, cap * head_dim * 4));
+    HIP_CHECK(hipMalloc(&pm, cap * 4));
+    HIP_CHECK(hipMalloc(&ps, cap * 4));
+    hipStream_t stream;
+    HIP_CHECK(hipStreamCreate(&stream));
+    struct Nodes { hipGraphNode_t store_kv, attention, merge; };
+    std::vector<Nodes> nodes(layers);
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    auto enqueue = [&](KVCache& cache, __half* qkv, __half* out, size_t start_pos, bool capture) {
+        for (size_t l = 0; l < layers; ++l) {
+            __half* a = qkv + l * total;
+            const bool apply = (l + 1) % 4 != 0;
+            launch_rope_and_store_kv(a, a + q_dim, a + q_dim + kv_dim, cache.get_k_cache(l),
+                                     cache.get_v_cache(l), rope.d_cos, rope.d_sin, 1, heads,
+                                     kv_heads, head_dim, total, total, start_pos, apply, stream);
+            if (capture) nodes[l].store_kv = last_captured_node(stream);
+            launch_causal_attention_decode_vectorized(
+                a, cache.get_k_cache(l), cache.get_v_cache(l), out + l * q_dim, po, pm, ps, 1,
+                start_pos + 1, start_pos, heads, kv_heads, head_dim, total, kv_dim, stream,
+                capture ? &nodes[l].attention : nullptr, capture ? &nodes[l].merge : nullptr);
+        }
+    };
+    bool all = true;
+    for (size_t step = 0; step < steps; ++step) {
+        const size_t start_pos = prompt + step;
+        HIP_CHECK(hipMemcpy(d_qkv_g, qkv_steps[step].data(), layers * total * 2, hipMemcpyHostToDevice));
+        HIP_CHECK(hipMemcpy(d_qkv_e, qkv_steps[step].data(), layers * total * 2, hipMemcpyHostToDevice));
+        if (!exec) {
+            HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeGlobal));
+            enqueue(graph_cache, d_qkv_g, d_out_g, start_pos, true);
+            HIP_CHECK(hipStreamEndCapture(stream, &graph));
+            HIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+        } else {
+            for (size_t l = 0; l < layers; ++l) {
+                update_rope_and_store_kv_node(exec, nodes[l].store_kv, start_pos, (l + 1) % 4 != 0);
+                update_causal_attention_decode_node(exec, nodes[l].attention, start_pos + 1);
+                update_merge_attention_decode_node(exec, nodes[l].merge, start_pos + 1);
+            }
+        }
+        HIP_CHECK(hipGraphLaunch(exec, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        enqueue(eager_cache, d_qkv_e, d_out_e, start_pos, false);
+        HIP_CHECK(hipStreamSynchronize(stream));
+        const auto og = download(d_out_g, layers * q_dim), oe = download(d_out_e, layers * q_dim);
+        const auto cg = download(graph_cache.get_k_cache(0), cache_init.size());
+        const auto ce = download(eager_cache.get_k_cache(0), cache_init.size());
+        const auto qg = download(d_qkv_g, layers * total), qe = download(d_qkv_e, layers * total);
+        const bool ok = same_bits(og.data(), oe.data(), og.size()) &&
+                        same_bits(cg.data(), ce.data(), cg.size()) &&
+                        same_bits(qg.data(), qe.data(), qg.size());
+        if (!ok) {
+            std::printf("  graph/eager mismatch at step %zu\n", step);
+            all = false;
+        }
+    }
+    HIP_CHECK(hipGraphExecDestroy(exec));
+    HIP_CHECK(hipGraphDestroy(graph));
+    HIP_CHECK(hipStreamDestroy(stream));
+    for (void* p : {(void*)d_qkv_g, (void*)d_qkv_e, (void*)d_out_g, (void*)d_out_e, (void*)po, (void*)pm, (void*)ps})
+        HIP_CHECK(hipFree(p));
+    report("graph_decode_step_node_patching", all);
+}
+
+}  // namespace
+
+int main() {
+    int dev = 0;
+    HIP_CHECK(hipSetDevice(dev));
+    test_flash_decode_kat();
+    test_rope_and_store_kv();
+    test_decode_vs_prefill_rows();
+    test_graph_decode_step();
+    std::printf("%d failure(s)\n", g_failures);
+    return g_failures;
+}
