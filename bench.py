@@ -21,6 +21,7 @@ the reference's PyTorch CPU attention (python/reference.py:61-96 restated with
 torch SDPA, fp16).  Inputs are seeded synthetic N(0, sigma) tensors.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+       python bench.py --profile   (eager launches for rocprofv3 counter passes)
 """
 from __future__ import annotations
 
@@ -224,7 +225,7 @@ def cpu_baselines(torch, quick):
     q = rng.standard_normal(Q_DIM).astype(np.float16).view(np.uint16)
     k = rng.standard_normal(L * KV_DIM).astype(np.float16).view(np.uint16)
     v = rng.standard_normal(L * KV_DIM).astype(np.float16).view(np.uint16)
-    calls = 2 if quick else 8
+    calls = 2 if quick else 24
     oracle.attention(q, k, v, 1, HQ, HKV, D, Q_DIM, KV_DIM, L, L - 1, causal=False)
     t0 = time.perf_counter()
     for _ in range(calls):
@@ -284,6 +285,51 @@ def cpu_baselines(torch, quick):
     return res
 
 
+def profile_workload(torch, A):
+    """Eager launches of every hot kernel at its headline shape, for hardware
+    counter passes (one dispatch per kernel call, no graph)."""
+    dev = torch.device("cuda:0")
+    L, nbuf = 32768, 8
+    q = rand16(torch, Q_DIM, 3)
+    ks = [rand16(torch, (L + 1) * KV_DIM, 4 + 2 * b) for b in range(nbuf)]
+    vs = [rand16(torch, (L + 1) * KV_DIM, 5 + 2 * b) for b in range(nbuf)]
+    po, pm, ps = A.decode_workspace(HQ, L, D, device=dev)
+    out = torch.empty(Q_DIM, dtype=torch.float16, device=dev)
+    for i in range(16):
+        A.decode(q, ks[i % nbuf], vs[i % nbuf], out, po, pm, ps, 1, L, L - 1, HQ, HKV, D, QKV,
+                 KV_DIM)
+    torch.cuda.synchronize()
+    log(f"profile: 16 decode calls L={L} (algorithmic {decode_bytes(L)} B each)")
+    del ks, vs
+    N = 8192
+    qkv = rand16(torch, N * QKV, 4, 0.5)
+    kc = rand16(torch, N * KV_DIM, 5, 0.5)
+    vc = rand16(torch, N * KV_DIM, 6, 0.5)
+    o = torch.empty(N * Q_DIM, dtype=torch.float16, device=dev)
+    for _ in range(3):
+        A.prefill(qkv, kc, vc, o, N, HQ, HKV, D, QKV, KV_DIM)
+    torch.cuda.synchronize()
+    log(f"profile: 3 prefill calls N={N}")
+    cos, sin = A.rope_tables(N, D, THETA)
+    dcos, dsin = cos.to(dev), sin.to(dev)
+    cache = torch.empty(2 * N * KV_DIM, dtype=torch.float16, device=dev)
+    lib = A.lib()
+    s, c = qkv.data_ptr(), cache.data_ptr()
+    for _ in range(3):
+        rc = lib.attn_rope_store_kv(s, s + 2 * Q_DIM, s + 2 * (Q_DIM + KV_DIM), c,
+                                    c + 2 * N * KV_DIM, dcos.data_ptr(), dsin.data_ptr(), N, HQ,
+                                    HKV, D, QKV, QKV, 0, 1, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+    torch.cuda.synchronize()
+    log(f"profile: 3 rope+append calls N={N} (algorithmic {rope_bytes(N)} B each)")
+    src = torch.empty(128 << 20, dtype=torch.float16, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("profile: 3 device copies of 256 MiB (reads 268435456 B, writes 268435456 B each)")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -291,6 +337,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, short CPU sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--profile", action="store_true",
+                    help="eager launches only, for rocprofv3 --pmc passes: 16 cold C3 decode "
+                         "calls, 3 C4 prefills, 3 RoPE+append at 8192 tokens and a 256 MiB "
+                         "device copy that calibrates the byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the attention hot path is "
@@ -305,6 +355,9 @@ def main():
     props = torch.cuda.get_device_properties(0)
     log(f"device {props.name} {props.gcnArchName} CUs={props.multi_processor_count}")
     steps, warmup = args.steps, args.warmup
+    if args.profile:
+        profile_workload(torch, A)
+        return
 
     # ---- headline: C3 decode at L=32768, cold (8 rotated KV buffers)
     L = 32768

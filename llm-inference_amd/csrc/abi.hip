@@ -188,6 +188,7 @@ int attn_prefill(const attn_f16_t* q, const attn_f16_t* k, const attn_f16_t* v,
     if (head_dim == 0) return 0;
     if (!fits_u32(seq_len) || !fits_u32(num_heads) || !fits_u32(head_dim))
         return (int)hipErrorInvalidValue;
+    if (!q || !k || !v || !out) return (int)hipErrorInvalidValue;
     PrefillArgs a{};
     a.q = reinterpret_cast<const f16*>(q);
     a.k = reinterpret_cast<const f16*>(k);
@@ -250,6 +251,7 @@ int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t
     if (num_heads % num_kv_heads != 0) return 0;
     if (!fits_u32(kv_len) || !fits_u32(num_heads) || !fits_u32(head_dim))
         return (int)hipErrorInvalidValue;
+    if (!q || !k_cache || !v_cache || !out) return (int)hipErrorInvalidValue;
     const size_t kvs = kv_stride ? kv_stride : num_kv_heads * head_dim;
     int device = 0;
     hipError_t e = hipGetDevice(&device);

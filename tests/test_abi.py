@@ -82,6 +82,10 @@ def test_invalid_arguments_are_errors(attn):
                                   0, 0, None) != 0
     assert lib.attn_set_option(b"no_such_option", 1) == -1
     assert lib.attn_update_decode_node(None, None, 0) != 0
+    # null data pointers are rejected before anything is launched
+    assert lib.attn_prefill(None, None, None, None, 8, 16, 4, 128, 0, 0, None) != 0
+    assert lib.attn_decode(None, None, None, None, None, None, None, 1, 5, 4, 16, 4, 128, 0, 0,
+                           None, None, None) != 0
 
 
 def test_decode_plan_respects_workspace_capacity(attn):
