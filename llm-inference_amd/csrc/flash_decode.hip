@@ -31,7 +31,8 @@
 //    batch needs no clamping and the prefetch past the end is free.
 //  * merge: grid = (Hq, D/16).  Each workgroup folds every split's partial
 //    for 16 output dims of one head: M = max_c m_c, l = sum_c 2^(m_c-M) l_c,
-//    out = sum_c 2^(m_c-M) acc_c / l (an online merge per thread, then LDS).
+//    out = sum_c 2^(m_c-M) acc_c / l (an online merge per thread over 16-byte
+//    partial loads, then LDS).
 //    The kernel boundary orders the partial writes before the merge reads;
 //    device-scope atomics/fences inside one kernel were measured to cost far
 //    more on the 8-XCD part than the extra launch.
@@ -221,67 +222,106 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     }
 }
 
-// grid (Hq, D/16), 256 threads: thread (cg, dl) folds splits c = cg, cg+16, ...
-// for dim d0 + dl with an online merge, then the 16 groups meet in LDS.
+// grid (Hq, D/16), 256 threads.  Thread (sl, q4) = (t / 4, t % 4) folds the
+// partials of splits c = sl, sl + 64, ... for dims d0 + 4q4 .. +3 with an
+// online merge; the 64 split lanes then meet in LDS.  All loads go through
+// range-checked buffer resources sized to this head's S partials, so splits
+// past S read as zero without branches (their maxima are replaced by -inf).
 constexpr int kMergeDims = 16;
-constexpr int kMergeGroups = 16;
-constexpr int kMergeRound = 16;  // splits per thread per round of loads
+constexpr int kMergeLanes = 64;  // split lanes per workgroup
+constexpr int kMergeRound = 4;   // splits per thread per round of loads
+
+__device__ __forceinline__ float buf_ldf(BufRsrc r, uint32_t byte_off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 0));
+}
+__device__ __forceinline__ f32x4 buf_ldf4(BufRsrc r, uint32_t byte_off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
+}
 
 __global__ __launch_bounds__(256) void flash_decode_merge(DecodeArgs a) {
-    __shared__ float s_m[kMergeGroups][kMergeDims];
-    __shared__ float s_l[kMergeGroups][kMergeDims];
-    __shared__ float s_a[kMergeGroups][kMergeDims];
+    __shared__ float s_m[kMergeLanes];
+    __shared__ float s_l[kMergeLanes];
+    __shared__ float s_w[kMergeLanes];
+    __shared__ float s_a[kMergeLanes][kMergeDims + 1];
+    __shared__ float s_num[256 / kMergeDims][kMergeDims];
+    __shared__ float s_den;
+    const uint32_t t = threadIdx.x;
     const uint32_t h = blockIdx.x;
-    const uint32_t dl = threadIdx.x % kMergeDims;
-    const uint32_t d = blockIdx.y * kMergeDims + dl;
-    const uint32_t cg = threadIdx.x / kMergeDims;
+    const uint32_t d0 = blockIdx.y * kMergeDims;
+    const uint32_t q4 = t & 3u;
+    const uint32_t sl = t >> 2;
     const uint32_t S = a.nsplit;
-    const float* pm = a.part_max + (uint64_t)h * S;
-    const float* ps = a.part_sum + (uint64_t)h * S;
-    const float* po = a.part_out + (uint64_t)h * S * kD + d;
-    float m = -INFINITY, l = 0.f, acc = 0.f;
-    // all loads of a round are issued before the fold: one memory latency
-    // per round (a single round for S <= 256)
-    for (uint32_t base = cg; base < S; base += kMergeGroups * kMergeRound) {
-        float mc[kMergeRound], lc[kMergeRound], ac[kMergeRound];
+    const BufRsrc rpm = make_rsrc(a.part_max + (uint64_t)h * S, S * 4u);
+    const BufRsrc rps = make_rsrc(a.part_sum + (uint64_t)h * S, S * 4u);
+    const BufRsrc rpo = make_rsrc(a.part_out + (uint64_t)h * S * kD, S * kD * 4u);
+    const uint32_t dbyte = (d0 + 4u * q4) * 4u;
+
+    float m = -INFINITY, l = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    // all loads of a round are issued before the fold (one round for S <= 256)
+    for (uint32_t base = sl; base < S; base += kMergeLanes * kMergeRound) {
+        float mc[kMergeRound], lc[kMergeRound];
+        f32x4 ac[kMergeRound];
 #pragma unroll
         for (int u = 0; u < kMergeRound; ++u) {
-            const uint32_t cc = base + (uint32_t)(kMergeGroups * u);
-            const bool ok = cc < S;
-            mc[u] = ok ? pm[cc] : -INFINITY;
-            lc[u] = ok ? ps[cc] : 0.f;
-            ac[u] = ok ? po[(uint64_t)cc * kD] : 0.f;
+            const uint32_t c = base + (uint32_t)(kMergeLanes * u);
+            mc[u] = buf_ldf(rpm, c * 4u);
+            lc[u] = buf_ldf(rps, c * 4u);
+            ac[u] = buf_ldf4(rpo, c * (kD * 4u) + dbyte);
         }
+#pragma unroll
+        for (int u = 0; u < kMergeRound; ++u)
+            if (base + (uint32_t)(kMergeLanes * u) >= S) mc[u] = -INFINITY;
         float mn = m;
 #pragma unroll
-        for (int u = 0; u < kMergeRound; ++u) mn = fmaxf(mn, mc[u]);
+        for (int u = 0; u < kMergeRound; ++u) mn = fmaxf(mn, mc[u]);  // split `base` is valid
         const float so = fast_exp2(m - mn);  // first round: 2^-inf = 0
         l *= so;
         acc *= so;
 #pragma unroll
         for (int u = 0; u < kMergeRound; ++u) {
-            const float sc = fast_exp2(mc[u] - mn);
+            const float sc = fast_exp2(mc[u] - mn);  // invalid splits: 0
             l += lc[u] * sc;
             acc += ac[u] * sc;
         }
         m = mn;
     }
-    s_m[cg][dl] = m;
-    s_l[cg][dl] = l;
-    s_a[cg][dl] = acc;
+    if (q4 == 0) {
+        s_m[sl] = m;  // lanes without splits: -inf, weight 0 below
+        s_l[sl] = l;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_a[sl][4 * q4 + e] = acc[e];
     __syncthreads();
-    if (cg == 0) {
-        float M = s_m[0][dl];
+    if (t < kMergeLanes) {  // wave 0: global max, weights, denominator
+        const float mi = s_m[t];
+        float mx = mi;
 #pragma unroll
-        for (int i = 1; i < kMergeGroups; ++i) M = fmaxf(M, s_m[i][dl]);
-        float num = 0.f, den = 0.f;
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, xor_lane(mx, o));
+        const float w = fast_exp2(mi - mx);
+        s_w[t] = w;
+        float den = w * s_l[t];
 #pragma unroll
-        for (int i = 0; i < kMergeGroups; ++i) {
-            const float w = fast_exp2(s_m[i][dl] - M);  // empty groups: 2^-inf = 0
-            num += w * s_a[i][dl];
-            den += w * s_l[i][dl];
+        for (int o = 32; o >= 1; o >>= 1) den += xor_lane(den, o);
+        if (t == 0) s_den = den;
+    }
+    __syncthreads();
+    {
+        const uint32_t dd = t % kMergeDims, grp = t / kMergeDims;  // 16 groups x 4 lanes
+        float num = 0.f;
+#pragma unroll
+        for (int k = 0; k < kMergeLanes / (256 / kMergeDims); ++k) {
+            const uint32_t i = grp * (kMergeLanes / (256 / kMergeDims)) + k;
+            num += s_w[i] * s_a[i][dd];
         }
-        a.out[(uint64_t)h * kD + d] = (f16)(num / den);
+        s_num[grp][dd] = num;
+    }
+    __syncthreads();
+    if (t < kMergeDims) {
+        float tot = 0.f;
+#pragma unroll
+        for (int g2 = 0; g2 < 256 / kMergeDims; ++g2) tot += s_num[g2][t];
+        a.out[(uint64_t)h * kD + d0 + t] = (f16)(tot / s_den);
     }
 }
 
