@@ -113,10 +113,12 @@ int attn_rope_tables(attn_f16_t* cos_out, attn_f16_t* sin_out, size_t max_seq_le
 /* Introspection for tests and benchmarks: the decode plan chosen for a shape
  * on the current device.  out[0] = path (0 generic; 1, 2, 3 = MFMA split
  * kernel serving 4, 2, 1 KV heads per workgroup), out[1] = splits of the
- * context, out[2] = keys per split, out[3] = threads per workgroup. */
+ * context, out[2] = keys per split, out[3] = threads per workgroup, out[4] =
+ * partial states per query head written to the workspace (at most
+ * ceil(kv_len / ATTN_KV_CHUNK)). */
 int attn_decode_plan(size_t kv_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
                      size_t kv_stride, const void* q, const void* k_cache,
-                     const void* v_cache, uint32_t out[4]);
+                     const void* v_cache, uint32_t out[5]);
 
 /* Prefill path chosen for a shape: 0 generic, 1 MFMA. */
 int attn_prefill_plan(const void* q, const void* k, const void* v, const void* out,

@@ -224,7 +224,7 @@ int attn_prefill(const attn_f16_t* q, const attn_f16_t* k, const attn_f16_t* v,
 
 int attn_decode_plan(size_t kv_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
                      size_t kv_stride, const void* q, const void* k_cache,
-                     const void* v_cache, uint32_t out[4]) {
+                     const void* v_cache, uint32_t out[5]) {
     if (!out || num_kv_heads == 0 || num_heads % num_kv_heads != 0 || kv_len == 0) return -1;
     int device = 0;
     (void)hipGetDevice(&device);
@@ -236,6 +236,7 @@ int attn_decode_plan(size_t kv_len, size_t num_heads, size_t num_kv_heads, size_
     out[1] = p.nsplit;
     out[2] = p.chunk;
     out[3] = p.block;
+    out[4] = p.nstate;
     return 0;
 }
 
@@ -304,6 +305,7 @@ int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t
     a.scale_log2 = scale_log2_for(head_dim);
     a.nsplit = p.nsplit;
     a.chunk = p.chunk;
+    a.nstate = p.nstate;
     e = launch_decode_split(a, p, stream);
     if (e != hipSuccess) return (int)e;
     if (attention_node) {
@@ -335,8 +337,9 @@ static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, siz
         params.extra = nullptr;
         return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
     }
-    const bool is_split =
-        params.func == decode_split_symbol(1) || params.func == decode_split_symbol(2);
+    const bool is_split = params.func == decode_split_symbol(1) ||
+                          params.func == decode_split_symbol(2) ||
+                          params.func == decode_split_symbol(3);
     const bool is_merge = params.func == decode_merge_symbol();
     if ((merge && !is_merge) || (!merge && !is_split)) return (int)hipErrorInvalidValue;
     DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(params.kernelParams[0]);

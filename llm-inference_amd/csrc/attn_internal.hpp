@@ -39,9 +39,9 @@ struct DecodeArgs {
     const f16* k;        // cache rows, kv_stride elements apart
     const f16* v;
     f16* out;            // [Hq][D] packed
-    float* part_out;     // [Hq][nsplit][D]   (workspace)
-    float* part_max;     // [Hq][nsplit]      (workspace, log2 domain)
-    float* part_sum;     // [Hq][nsplit]      (workspace)
+    float* part_out;     // [Hq][nstate][D]   (workspace)
+    float* part_max;     // [Hq][nstate]      (workspace, log2 domain)
+    float* part_sum;     // [Hq][nstate]      (workspace)
     uint64_t kv_stride;
     uint32_t kv_len;     // patched per decode step
     uint32_t num_heads;
@@ -50,6 +50,7 @@ struct DecodeArgs {
     uint32_t head_dim;
     uint32_t nsplit;     // context splits per KV head (patched)
     uint32_t chunk;      // keys per split (patched)
+    uint32_t nstate;     // partial states per query head (patched)
     float scale_log2;    // log2(e) / sqrt(D)
 };
 
@@ -57,6 +58,7 @@ struct DecodePlan {
     int path;          // 0 = generic (any D, any stride); 1/2/3 = MFMA split with 4/2/1 KV heads per workgroup + merge
     uint32_t nsplit;
     uint32_t chunk;
+    uint32_t nstate;   // partial states per query head written to the workspace
     uint32_t block;    // threads per split workgroup
 };
 

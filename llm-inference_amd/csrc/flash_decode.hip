@@ -213,7 +213,7 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
             num += wt * s_acc[w][qn][d];
             den += wt * s_l[w][qn];
         }
-        const uint64_t st = (uint64_t)((blockIdx.y * HPW + hl) * G + qn) * a.nsplit + c;
+        const uint64_t st = (uint64_t)((blockIdx.y * HPW + hl) * G + qn) * a.nstate + c;
         a.part_out[st * kD + d] = num;
         if (d == 0) {
             a.part_max[st] = M;
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(256) void flash_decode_merge(DecodeArgs a) {
     const uint32_t d0 = blockIdx.y * kMergeDims;
     const uint32_t q4 = t & 3u;
     const uint32_t sl = t >> 2;
-    const uint32_t S = a.nsplit;
+    const uint32_t S = a.nstate;
     const BufRsrc rpm = make_rsrc(a.part_max + (uint64_t)h * S, S * 4u);
     const BufRsrc rps = make_rsrc(a.part_sum + (uint64_t)h * S, S * 4u);
     const BufRsrc rpo = make_rsrc(a.part_out + (uint64_t)h * S * kD, S * kD * 4u);
@@ -342,7 +342,7 @@ const void* decode_merge_symbol() { return reinterpret_cast<const void*>(&flash_
 DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_heads,
                        uint32_t head_dim, uint64_t kv_stride, const void* q, const void* k,
                        const void* v, int device) {
-    DecodePlan p{0, 1, kv_len, 256};
+    DecodePlan p{0, 1, kv_len, 1, 256};
     const uint32_t G = num_heads / num_kv_heads;
     const bool mfma_ok = head_dim == kD && G >= 1 && G <= 16 && kv_stride % 8 == 0 &&
                          kv_stride * 2 <= 0x40000000ull && aligned16(q) && aligned16(k) &&
@@ -366,6 +366,7 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
     nsplit = (kv_len + chunk - 1) / chunk;
     p.nsplit = nsplit;
     p.chunk = chunk;
+    p.nstate = nsplit;  // one folded state per split and query head
     return p;
 }
 
@@ -374,6 +375,7 @@ void replan_decode(DecodeArgs& a, int device) {
                                      a.kv_stride, a.q, a.k, a.v, device);
     a.nsplit = p.nsplit;
     a.chunk = p.chunk;
+    a.nstate = p.nstate;
 }
 
 hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {

@@ -159,11 +159,12 @@ def decode(q, k_cache, v_cache, out, partial_out, partial_max, partial_sum, quer
 
 def decode_plan(kv_len, num_heads, num_kv_heads, head_dim, kv_stride=0, q=None, k=None,
                 v=None):
-    out = (ctypes.c_uint32 * 4)()
+    out = (ctypes.c_uint32 * 5)()
     rc = lib().attn_decode_plan(kv_len, num_heads, num_kv_heads, head_dim, kv_stride,
                                 _ptr(q) or 256, _ptr(k) or 256, _ptr(v) or 256, out)
     _check(rc, "attn_decode_plan")
-    return {"path": out[0], "nsplit": out[1], "chunk": out[2], "block": out[3]}
+    return {"path": out[0], "nsplit": out[1], "chunk": out[2], "block": out[3],
+            "nstate": out[4]}
 
 
 def prefill_plan(q, k, v, out, num_heads, num_kv_heads, head_dim, q_stride=0, kv_stride=0):

@@ -89,16 +89,24 @@ def test_invalid_arguments_are_errors(attn):
 
 
 def test_decode_plan_respects_workspace_capacity(attn):
-    # whatever the split plan, the partial states fit in the reference-sized
-    # workspace Hq * ceil(L / 12)
-    for L in (1, 12, 13, 100, 129, 254, 1000, 4096, 32768, 65536, 131072):
-        for hq, hkv in ((16, 4), (4, 4), (2, 1), (16, 1), (32, 8)):
-            p = attn.decode_plan(L, hq, hkv, 128)
-            cap = hq * ((L + 11) // 12)
-            assert p["path"] == (1 if hkv % 4 == 0 else 2 if hkv % 2 == 0 else 3)
-            assert p["nsplit"] >= 1 and p["chunk"] * p["nsplit"] >= L
-            assert (p["nsplit"] - 1) * p["chunk"] < L  # no empty split
-            assert hq * p["nsplit"] <= cap
+    # whatever the split plan, the partial states (one per split) fit in the
+    # reference-sized workspace Hq * ceil(L / 12)
+    lengths = (1, 2, 12, 13, 31, 32, 33, 63, 64, 65, 100, 129, 254, 255, 256, 257, 1000, 4096,
+               32768, 65536, 131072)
+    try:
+        for splits in (0, 1, 2, 3, 64, 256, 1024):
+            attn.set_option("decode_splits", splits)
+            for L in lengths:
+                for hq, hkv in ((16, 4), (4, 4), (2, 1), (16, 1), (32, 8), (8, 2)):
+                    p = attn.decode_plan(L, hq, hkv, 128)
+                    hpw = 4 if hkv % 4 == 0 else 2 if hkv % 2 == 0 else 1
+                    assert p["path"] == {4: 1, 2: 2, 1: 3}[hpw]
+                    assert p["nsplit"] >= 1 and p["chunk"] * p["nsplit"] >= L
+                    assert (p["nsplit"] - 1) * p["chunk"] < L  # no empty split
+                    assert p["nstate"] == p["nsplit"]
+                    assert hq * p["nstate"] <= hq * ((L + 11) // 12), (splits, L, hq, hkv, p)
+    finally:
+        attn.set_option("decode_splits", 0)
     # head_dim != 128 or an odd stride takes the generic kernel
     assert attn.decode_plan(257, 4, 2, 32)["path"] == 0
     assert attn.decode_plan(257, 4, 2, 128, kv_stride=2 * 128 + 17)["path"] == 0

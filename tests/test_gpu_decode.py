@@ -215,3 +215,50 @@ def test_decode_graph_node_update(attn, gpu):
             assert_close(host(out_g), expected(q, k, v, L), 2e-3, 1e-2, f"graph L={L}")
     finally:
         hipgraph.destroy(graph, exe)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(16, 2), (8, 1)])
+def test_decode_graph_node_update_other_paths(attn, gpu, Hq, Hkv):
+    """The node patchers re-plan the 2- and 1-KV-head-per-workgroup kernels
+    too (paths 2 and 3): replays equal eager launches bit for bit."""
+    import ctypes
+
+    from attn_mi355x import hipgraph
+    D, Lmax = 128, 9000
+    rng = np.random.default_rng(Hq * 10 + Hkv)
+    q = rng.standard_normal(Hq * D).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal(Lmax * Hkv * D).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal(Lmax * Hkv * D).astype(np.float16).view(np.uint16)
+    dq, dk, dv = dev(q, gpu), dev(k, gpu), dev(v, gpu)
+    states = attn.decode_workspace_states(Hq, Lmax)
+    po, pm, ps = (torch.empty(states * D, device=gpu), torch.empty(states, device=gpu),
+                  torch.empty(states, device=gpu))
+    po2, pm2, ps2 = po.clone(), pm.clone(), ps.clone()
+    out_g = torch.empty(Hq * D, dtype=torch.float16, device=gpu)
+    out_e = torch.empty(Hq * D, dtype=torch.float16, device=gpu)
+    assert attn.decode_plan(Lmax, Hq, Hkv, D)["path"] == (2 if Hkv == 2 else 3)
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    anode, mnode = ctypes.c_void_p(), ctypes.c_void_p()
+    L0 = 50
+    with torch.cuda.stream(stream):
+        hipgraph.begin_capture(sp)
+        rc = attn.lib().attn_decode(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), out_g.data_ptr(),
+                                    po.data_ptr(), pm.data_ptr(), ps.data_ptr(), 1, L0, L0 - 1, Hq,
+                                    Hkv, D, 0, 0, sp, ctypes.byref(anode), ctypes.byref(mnode))
+        assert rc == 0
+        graph, exe = hipgraph.end_capture(sp)
+    try:
+        for L in (50, 777, 4096, 8999):
+            assert attn.lib().attn_update_decode_node(exe, anode, L) == 0
+            assert attn.lib().attn_update_merge_node(exe, mnode, L) == 0
+            hipgraph.launch(exe, sp)
+            hipgraph.synchronize(sp)
+            attn.decode(dq, dk, dv, out_e, po2, pm2, ps2, 1, L, L - 1, Hq, Hkv, D)
+            torch.cuda.synchronize()
+            print(f"[case] decode graph Hq={Hq} Hkv={Hkv} L={L}", flush=True)
+            assert np.array_equal(host(out_g), host(out_e)), (Hq, Hkv, L)
+            assert_close(host(out_g), expected(q, k, v, L, Hq, Hkv, D), 2e-3, 1e-2,
+                         f"graph {Hq}/{Hkv} L={L}")
+    finally:
+        hipgraph.destroy(graph, exe)
