@@ -8,7 +8,7 @@ prefill-attn TFLOPS @8K tokens"):
                bytes 2048*L + 8192 per call, KV rotated over 8 buffers
                (8 x 67 MB > 256 MB Infinity Cache) so every call streams HBM.
   prefill    = causal prefill TFLOPS at N = 8192 (config C4), algorithmic
-               FLOPs 4096*N*(N+1).
+               FLOPs 4096*N*(N+1); best of 3 timed runs after 40 warm-up calls.
 A "step" is one decode-attention call over one KV buffer.  The K timed steps
 are one HIP-graph replay of K captured decode launches (the engine's decode
 also replays a graph, model_inference.hpp:96-126), bracketed by
@@ -116,7 +116,9 @@ def bench_decode(torch, A, hipgraph, L, nbuf, steps, warmup, seed=3):
     return ms
 
 
-def bench_prefill(torch, A, N, steps, warmup, seed=4, sigma=0.5):
+def bench_prefill(torch, A, N, steps, warmup, seed=4, sigma=0.5, trials=3):
+    """Prefill ms per call: `warmup` untimed calls (the clock ramps for tens of
+    calls under MFMA load), then the best of `trials` timed runs of `steps`."""
     dev = torch.device("cuda:0")
     qkv = rand16(torch, N * QKV, seed, sigma)
     kc = rand16(torch, N * KV_DIM, seed + 1, sigma)
@@ -126,14 +128,17 @@ def bench_prefill(torch, A, N, steps, warmup, seed=4, sigma=0.5):
     for _ in range(warmup):
         A.prefill(qkv, kc, vc, out, N, HQ, HKV, D, QKV, KV_DIM)
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
-        A.prefill(qkv, kc, vc, out, N, HQ, HKV, D, QKV, KV_DIM)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    best = float("inf")
+    for _ in range(trials):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            A.prefill(qkv, kc, vc, out, N, HQ, HKV, D, QKV, KV_DIM)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) / steps)
+    return best
 
 
 def bench_rope(torch, A, hipgraph, N, nbuf, steps, warmup, rotate=True, seed=6):
@@ -371,8 +376,8 @@ def main():
 
     # ---- C4 prefill at 8192 tokens
     N = 8192
-    pf_steps = max(5, min(50, steps // 4))
-    pms = bench_prefill(torch, A, N, pf_steps, 20)  # warm-up lets the clock settle
+    pf_steps = max(5, min(20, steps // 10))
+    pms = bench_prefill(torch, A, N, pf_steps, 40)
     tflops = prefill_flops(N) / (pms * 1e-3) / 1e12
     log(f"prefill N={N}: {pms * 1e3:.1f} us  {tflops:.1f} TFLOP/s ({100 * tflops / PEAK_FP16_TFLOPS:.1f}% of fp16 peak)")
 
