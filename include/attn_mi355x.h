@@ -127,8 +127,7 @@ int attn_prefill_plan(const void* q, const void* k, const void* v, const void* o
 
 /* Process-wide switches for tests and benchmarks (not needed in production):
  * "decode_force_generic", "decode_splits" (0 = automatic),
- * "prefill_force_generic", "prefill_waves" (4 or 8 waves per workgroup;
- * 0 = 8).  Returns 0 or -1 for an unknown name. */
+ * "prefill_force_generic".  Returns 0 or -1 for an unknown name. */
 int attn_set_option(const char* name, long value);
 
 /* Library build identification (static string). */

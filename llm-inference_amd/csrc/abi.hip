@@ -72,7 +72,6 @@ int attn_set_option(const char* name, long value) {
     if (!std::strcmp(name, "decode_force_generic")) which = kOptDecodeForceGeneric;
     else if (!std::strcmp(name, "decode_splits")) which = kOptDecodeSplits;
     else if (!std::strcmp(name, "prefill_force_generic")) which = kOptPrefillForceGeneric;
-    else if (!std::strcmp(name, "prefill_waves")) which = kOptPrefillWaves;
     if (which < 0) return -1;
     g_options[which].store(value, std::memory_order_relaxed);
     return 0;

@@ -121,7 +121,6 @@ enum Option {
     kOptDecodeForceGeneric = 0,
     kOptDecodeSplits = 1,        // 0 = automatic
     kOptPrefillForceGeneric = 2,
-    kOptPrefillWaves = 3,        // 4 or 8 waves per workgroup (0 = 8)
     kOptCount = 8
 };
 long get_option(int which);

@@ -8,22 +8,27 @@
 // MFMA path (D = 128, Hq/Hkv a multiple of 4, 16-byte aligned rows):
 //  * workgroup = 64 query tokens of 4 query heads sharing one KV head, as 8
 //    waves (two per head, 32 queries each, 2 waves per SIMD so one wave's
-//    softmax overlaps the other's MFMAs; everything stays in VGPRs) or, as an
-//    option, 4 waves of 64 queries (each LDS operand feeds two MFMAs).
+//    softmax overlaps the other's MFMAs); Q, S and O stay in VGPRs.
 //  * K and V of a 64-key tile are staged in LDS once per workgroup and shared
-//    by the 4 heads (the reference re-reads them per head).  V is stored
-//    transposed (V^T[dim][key]) with the keys of every 16-key MFMA step in the
-//    order the S^T accumulator produces them, so P never leaves registers.
+//    by the 4 heads (the reference re-reads them per head), copied straight
+//    from global memory into LDS by buffer_load ... lds (no VGPRs, no LDS
+//    stores).  Rows are padded (K 272 B, V 288 B) so the MFMA operand reads
+//    are free of bank conflicts; a DMA instruction writes 1 KiB of LDS and
+//    the lanes that land on padding fetch a harmless copy of a row's first
+//    16 bytes.  Rows past N read as zero through the buffer range check.
 //  * S^T = K . Q^T with v_mfma_f32_32x32x16_f16: keys are MFMA rows, queries
 //    columns, so each lane holds one query's scores and the online softmax
 //    (running max, running sum, rescale) is per lane plus one xor-32 exchange.
 //  * O^T = V^T . P^T on the same MFMA; O^T stays in 64 accumulator registers.
+//    The V^T operand comes from row-major V through ds_read_b64_tr_b16 (two
+//    4-key transposing reads per operand), with the keys in the order the
+//    S^T accumulator produces them, so P never leaves registers.
 //  * Causal tile skipping: query tile i visits key tiles 0..i only; the
 //    diagonal tile is masked.  Tiles are handed out longest-first and the
 //    four head groups of one KV head are kept on the same pair of XCDs so the
 //    KV head's K/V stays in one L2.
-//  * K/V tile j+1 is prefetched into registers while tile j is computed; two
-//    LDS buffers, one barrier per tile.
+//  * Tile j+1 is copied into the other LDS buffer while tile j is computed;
+//    one barrier per tile.
 #include "attn_internal.hpp"
 
 #include <type_traits>
@@ -33,10 +38,20 @@ namespace attn {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kBM = 64;        // query tokens per workgroup (per wave)
+constexpr int kBM = 64;        // query tokens per workgroup
 constexpr int kBN = 64;        // keys per tile
-constexpr int kKP = kD + 8;    // K tile row pitch (halves): conflict-free 16 B reads
-constexpr int kVP = kBN + 8;   // V^T tile row pitch (halves)
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kKP = kD + 8;    // K row pitch (halves): conflict-free 16 B A-operand reads
+constexpr int kVP = kD + 16;   // V row pitch (halves): conflict-free transposing reads
+constexpr int kKChunks = kKP / 8;             // 16-byte LDS chunks per K row (17)
+constexpr int kVChunks = kVP / 8;             // ... per V row (18)
+constexpr int kKDma = kBN * kKChunks / 64;    // 1 KiB DMA instructions per K tile (17)
+constexpr int kVDma = kBN * kVChunks / 64;    // ... per V tile (18)
+constexpr int kDmaPerWave = (kVDma + kWaves - 1) / kWaves;  // 3
+
+#define LDS_AS __attribute__((address_space(3)))
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f16x8 lds16(const f16* p) {
     return *reinterpret_cast<const f16x8*>(p);
@@ -44,6 +59,13 @@ __device__ __forceinline__ f16x8 lds16(const f16* p) {
 
 __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Four fp16 of one LDS column: lane i of each 16-lane group receives element
+// i of the 4-element chunks its group addresses, from chunks i/4, 4 + i/4, ...
+__device__ __forceinline__ f16x4 lds_tr4(const f16* p) {
+    const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS s16x4*)(const LDS_AS void*)p);
+    return __builtin_bit_cast(f16x4, r);
 }
 
 // blockIdx -> (head quad, query tile), longest tiles first, head quads pinned
@@ -72,18 +94,13 @@ __device__ __forceinline__ bool map_block(uint32_t bid, uint32_t quads, uint32_t
 // fp16 and the O^T accumulators are rarely touched by VALU code.
 constexpr float kRescaleSlack = 8.0f;
 
-// NT 32-query column tiles per wave.  NT = 2: 4 waves (one per grouped head,
-// 64 queries each, 1 wave per SIMD); NT = 1: 8 waves (two per head, 32
-// queries each, 2 waves per SIMD so one wave's softmax overlaps the other's
-// MFMAs).  Either way a workgroup covers 64 query tokens of 4 heads.
-template <int NT>
-__global__ __launch_bounds__(256 * (2 / NT), 1) void prefill_d128(PrefillArgs a) {
-    constexpr int kWaves = 4 * (2 / NT);
-    constexpr int kThreads = 64 * kWaves;
-    constexpr int kKChunks = (kBN * kD / 8) / kThreads;  // 16 B K chunks per thread
-    constexpr int kVKeys = (kBN * kD / 8) / kThreads;    // V keys per thread (x 8 dims)
-    __shared__ __attribute__((aligned(16))) f16 kt[2][kBN * kKP];
-    __shared__ __attribute__((aligned(16))) f16 vt[2][kD * kVP];
+__global__ __launch_bounds__(kThreads, 1) void prefill_d128(PrefillArgs a) {
+    // two LDS buffers per operand as distinct objects, so the compiler can
+    // tell a DMA into one buffer from the reads of the other
+    __shared__ __attribute__((aligned(16))) f16 kt0[kBN * kKP];
+    __shared__ __attribute__((aligned(16))) f16 kt1[kBN * kKP];
+    __shared__ __attribute__((aligned(16))) f16 vt0[kBN * kVP];
+    __shared__ __attribute__((aligned(16))) f16 vt1[kBN * kVP];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -97,205 +114,181 @@ __global__ __launch_bounds__(256 * (2 / NT), 1) void prefill_d128(PrefillArgs a)
     const uint32_t head = 4u * quad + (uint32_t)(wave & 3);
     const uint32_t g = (4u * quad) / a.group;
     const uint32_t N = a.seq_len;
-    const uint32_t q0 = tile * kBM + 32u * NT * (uint32_t)(wave >> 2);  // this wave's first query
+    const uint32_t q0 = tile * kBM + 32u * (uint32_t)(wave >> 2);  // this wave's first query
     const uint32_t q_row_bytes = (uint32_t)(a.q_stride * 2);
     const uint32_t kv_row_bytes = (uint32_t)(a.kv_stride * 2);
 
-    // buffer views: rows past N read as zero (no guards needed)
-    const BufRsrc rq = make_rsrc(a.q + (uint64_t)head * kD, (N - 1) * q_row_bytes + kD * 2);
-    const BufRsrc rk = make_rsrc(a.k + (uint64_t)g * kD, (N - 1) * kv_row_bytes + kD * 2);
-    const BufRsrc rv = make_rsrc(a.v + (uint64_t)g * kD, (N - 1) * kv_row_bytes + kD * 2);
-
-    // Q^T B operands: lane (hh, n) of column tile nt holds
-    // Q[q0 + 32nt + n][head][16s + 8hh .. +7] for k-step s.
-    f16x8 qb[NT][8];
+    // Q^T B operands: lane (hh, n) holds Q[q0 + n][head][16s + 8hh .. +7] for
+    // k-step s; rows past N read as zero
+    const BufRsrc rq = make_rsrc(a.q + (uint64_t)head * kD,
+                                 __builtin_amdgcn_readfirstlane((N - 1) * q_row_bytes + kD * 2));
+    f16x8 qb[8];
+    {
+        const uint32_t off = (q0 + n) * q_row_bytes + 16u * hh;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const uint32_t off = (q0 + 32u * nt + n) * q_row_bytes + 16u * hh;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) qb[nt][s] = buf_ld16(rq, off + 32u * s);
+        for (int s = 0; s < 8; ++s) qb[s] = buf_ld16(rq, off + 32u * s);
     }
 
-    f32x16 o[NT][4];
+    f32x16 o[4];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[nt][dt] = f32x16{};
-    float m_used[NT], l_run[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        m_used[nt] = -INFINITY;
-        l_run[nt] = 0.f;
-    }
+    for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
+    float m_used = -INFINITY, l_run = 0.f;
 
-    // global -> register staging of one 64-key tile: K as 16 B chunks, V as
-    // kVKeys consecutive keys x 8 dims per thread (transposed on the LDS store)
-    constexpr uint32_t kKeyGroups = kBN / kVKeys;
-    const uint32_t kgrp = tid % kKeyGroups;  // keys kVKeys*kgrp ..
-    const uint32_t dg = tid / kKeyGroups;    // dims 8dg..8dg+7
-    f16x8 kr[kKChunks], vr[kVKeys];
-    auto gload = [&](uint32_t kv0) {
+    // LDS-DMA staging.  DMA instruction i of a tile fills LDS bytes
+    // [1024 i, 1024 i + 1024) of the buffer; lane L writes 16-byte chunk
+    // q = 64 i + L = row * chunks + c, fetched from key row `row`, bytes 16c
+    // (c past the row's 16 data chunks is padding: bytes 0..15 again).  Wave w
+    // issues instructions w, w + 8, w + 16.
+    uint32_t koff[kDmaPerWave], voff[kDmaPerWave];
 #pragma unroll
-        for (int i = 0; i < kKChunks; ++i) {
-            const uint32_t e = (uint32_t)i * kThreads + tid;
-            kr[i] = buf_ld16(rk, (kv0 + (e >> 4)) * kv_row_bytes + 16u * (e & 15u));
-        }
+    for (int t = 0; t < kDmaPerWave; ++t) {
+        const uint32_t q = (uint32_t)(wave + kWaves * t) * 64u + (uint32_t)lane;
+        const uint32_t kr = q / kKChunks, kc = q % kKChunks;
+        const uint32_t vr = q / kVChunks, vc = q % kVChunks;
+        koff[t] = kr * kv_row_bytes + (kc < 16 ? kc : 0u) * 16u;
+        voff[t] = vr * kv_row_bytes + (vc < 16 ? vc : 0u) * 16u;
+    }
+    const f16* kbase = a.k + (uint64_t)g * kD;
+    const f16* vbase = a.v + (uint64_t)g * kD;
+    auto stage = [&](uint32_t kv0, f16* kt, f16* vt) {
+        // resources start at row kv0 and end at row N - 1
+        const uint32_t rows = N > kv0 ? N - kv0 : 0u;
+        const uint32_t bytes =
+            __builtin_amdgcn_readfirstlane(rows ? (rows - 1u) * kv_row_bytes + kD * 2 : 0u);
+        const BufRsrc rk = make_rsrc(kbase + (uint64_t)kv0 * a.kv_stride, bytes);
+        const BufRsrc rv = make_rsrc(vbase + (uint64_t)kv0 * a.kv_stride, bytes);
 #pragma unroll
-        for (int r = 0; r < kVKeys; ++r)
-            vr[r] = buf_ld16(rv, (kv0 + kVKeys * kgrp + r) * kv_row_bytes + 16u * dg);
-    };
-    // key 16ks + 8b + 4h + r sits in V^T slot ks*16 + h*8 + 4b + r: the order
-    // in which S^T tile ks/2 presents keys to PV k-step ks
-    const uint32_t key0 = kVKeys * kgrp;
-    const uint32_t vslot = (key0 >> 4) * 16u + ((key0 >> 2) & 1u) * 8u + ((key0 >> 3) & 1u) * 4u +
-                           (key0 & 3u);
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < kKChunks; ++i) {
-            const uint32_t e = (uint32_t)i * kThreads + tid;
-            *reinterpret_cast<f16x8*>(&kt[buf][(e >> 4) * kKP + 8u * (e & 15u)]) = kr[i];
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if constexpr (kVKeys == 4) {
-                f16x4 w;
-                w[0] = vr[0][j];
-                w[1] = vr[1][j];
-                w[2] = vr[2][j];
-                w[3] = vr[3][j];
-                *reinterpret_cast<f16x4*>(&vt[buf][(8u * dg + j) * kVP + vslot]) = w;
-            } else {
-                f16x2 w;
-                w[0] = vr[0][j];
-                w[1] = vr[1][j];
-                *reinterpret_cast<f16x2*>(&vt[buf][(8u * dg + j) * kVP + vslot]) = w;
-            }
+        for (int t = 0; t < kDmaPerWave; ++t) {
+            const int i = wave + kWaves * t;
+            if (i < kKDma)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rk, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)kt + 1024 * i), 16,
+                    (int)koff[t], 0, 0, 0);
+            if (i < kVDma)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rv, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)vt + 1024 * i), 16,
+                    (int)voff[t], 0, 0, 0);
         }
     };
+    // the DMA writes become visible to the workgroup after the vmcnt wait and
+    // the barrier that follows it
+    auto publish = [&]() {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+    };
+
+    // transposing-read address of lane (hh, n): group grp = lane / 16 holds
+    // dims 16 (grp & 1) + 0..15 of a 32-dim tile; its lane j addresses key
+    // 4 hh + j / 4 (+ the k-step and half offsets), dims 4 (j & 3) + 0..3
+    const uint32_t grp = (uint32_t)lane >> 4, jl = (uint32_t)lane & 15u;
+    const uint32_t vrd = (4u * hh + (jl >> 2)) * kVP + 16u * (grp & 1u) + 4u * (jl & 3u);
 
     // one 64-key tile: S^T = K . Q^T, online softmax, O^T += V^T . P^T
-    auto tile_step = [&](int buf, uint32_t j, auto diag_tag) {
+    auto tile_step = [&](const f16* kt, const f16* vt, uint32_t j, auto diag_tag) {
         constexpr bool kDiag = decltype(diag_tag)::value;
-        f32x16 s[NT][2];
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) s[nt][mt] = f32x16{};
+        f32x16 s[2] = {f32x16{}, f32x16{}};
         // K operands are read one k-step ahead of their MFMAs
-        const f16* kbuf = &kt[buf][n * kKP + 8 * hh];
+        const f16* kb = kt + n * kKP + 8 * hh;
         f16x8 ka[2][2];
-        ka[0][0] = lds16(kbuf);
-        ka[0][1] = lds16(kbuf + 32 * kKP);
+        ka[0][0] = lds16(kb);
+        ka[0][1] = lds16(kb + 32 * kKP);
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             const int cur = ks & 1;
             if (ks + 1 < 8) {
-                ka[cur ^ 1][0] = lds16(kbuf + 16 * (ks + 1));
-                ka[cur ^ 1][1] = lds16(kbuf + 32 * kKP + 16 * (ks + 1));
+                ka[cur ^ 1][0] = lds16(kb + 16 * (ks + 1));
+                ka[cur ^ 1][1] = lds16(kb + 32 * kKP + 16 * (ks + 1));
             }
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) s[nt][mt] = mfma32(ka[cur][mt], qb[nt][ks], s[nt][mt]);
+            for (int mt = 0; mt < 2; ++mt) s[mt] = mfma32(ka[cur][mt], qb[ks], s[mt]);
         }
-        float m_tile[NT];
+        float mx = -INFINITY;
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            float mx = -INFINITY;
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    float x = s[nt][mt][i];
-                    if constexpr (kDiag) {
-                        const uint32_t query = q0 + 32u * nt + n;
-                        const uint32_t key = j * kBN + 32u * mt + 8u * (i >> 2) + 4u * hh + (i & 3);
-                        if (key > query || key >= N) x = -INFINITY;
-                        s[nt][mt][i] = x;
-                    }
-                    mx = fmaxf(mx, x);
+            for (int i = 0; i < 16; ++i) {
+                float x = s[mt][i];
+                if constexpr (kDiag) {
+                    const uint32_t query = q0 + n;
+                    const uint32_t key = j * kBN + 32u * mt + 8u * (i >> 2) + 4u * hh + (i & 3);
+                    if (key > query || key >= N) x = -INFINITY;
+                    s[mt][i] = x;
                 }
-            mx = fmaxf(mx, xor_lane(mx, 32));
-            m_tile[nt] = mx * a.scale_log2;
-        }
-        // one (rarely taken) block rescales every column tile, so no part of
-        // it is speculated into the common path
-        bool need[NT];
-        bool any = false;
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            need[nt] = m_tile[nt] > m_used[nt] + kRescaleSlack;
-            any = any || need[nt];
-        }
-        if (__any(any)) {
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const float mn = need[nt] ? m_tile[nt] : m_used[nt];
-                const float al = fast_exp2(m_used[nt] - mn);
-                l_run[nt] *= al;
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) o[nt][dt] *= al;
-                m_used[nt] = mn;
+                mx = fmaxf(mx, x);
             }
-        }
-        float mneg[NT], psum[NT];
+        mx = fmaxf(mx, xor_lane(mx, 32));
+        const float m_tile = mx * a.scale_log2;
+        // one (rarely taken) block rescales, so none of it is speculated into
+        // the common path
+        if (__any(m_tile > m_used + kRescaleSlack)) {
+            const float mn = (m_tile > m_used + kRescaleSlack) ? m_tile : m_used;
+            const float al = fast_exp2(m_used - mn);
+            l_run *= al;
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            mneg[nt] = -m_used[nt];
-            psum[nt] = 0.f;
+            for (int dt = 0; dt < 4; ++dt) o[dt] *= al;
+            m_used = mn;
         }
+        const float mneg = -m_used;
+        float psum = 0.f;
         // P one 16-key MFMA step at a time, consumed at once by that step's
-        // PV MFMAs: exps of step ks+1 overlap the MFMAs of step ks
-        const f16* vbuf = &vt[buf][n * kVP + 8 * hh];
+        // PV MFMAs: exps of step ks+1 overlap the MFMAs of step ks.  Step ks
+        // covers keys 32 (ks / 2) + 16 (ks % 2) + 8 (e / 4) + 4 hh + e % 4.
+        const f16* vb = vt + vrd;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
+            const int koffs = (32 * (ks >> 1) + 16 * (ks & 1)) * kVP;
             f16x8 va[4];
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) va[dt] = lds16(vbuf + 32 * dt * kVP + 16 * ks);
-            f16x8 pb[NT];
+            for (int dt = 0; dt < 4; ++dt) {
+                const f16x4 lo = lds_tr4(vb + koffs + 32 * dt);
+                const f16x4 hi = lds_tr4(vb + koffs + 8 * kVP + 32 * dt);
+                va[dt] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+            f16x8 pb;
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
+            for (int r = 0; r < 8; ++r)
+                pb[r] = (f16)fast_exp2(__builtin_fmaf(s[ks >> 1][8 * (ks & 1) + r], a.scale_log2, mneg));
+            // row sum of the fp16 weights the PV product uses, two per
+            // v_dot2_f32_f16 (fp32 accumulate)
 #pragma unroll
-                for (int r = 0; r < 8; ++r)
-                    pb[nt][r] = (f16)fast_exp2(__builtin_fmaf(s[nt][ks >> 1][8 * (ks & 1) + r],
-                                                              a.scale_log2, mneg[nt]));
-                // row sum of the fp16 weights the PV product uses, two per
-                // v_dot2_f32_f16 (fp32 accumulate)
-#pragma unroll
-                for (int r = 0; r < 8; r += 2) {
-                    const f16x2 pair = {pb[nt][r], pb[nt][r + 1]};
-                    psum[nt] = __builtin_amdgcn_fdot2(pair, f16x2{(f16)1.0f, (f16)1.0f}, psum[nt], false);
-                }
+            for (int r = 0; r < 8; r += 2) {
+                const f16x2 pair = {pb[r], pb[r + 1]};
+                psum = __builtin_amdgcn_fdot2(pair, f16x2{(f16)1.0f, (f16)1.0f}, psum, false);
             }
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) o[nt][dt] = mfma32(va[dt], pb[nt], o[nt][dt]);
+            for (int dt = 0; dt < 4; ++dt) o[dt] = mfma32(va[dt], pb, o[dt]);
         }
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) l_run[nt] += psum[nt];
+        l_run += psum;
     };
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    // full tiles 0..tile-1 need no mask; tile `tile` holds the diagonal
-    for (uint32_t j = 0; j < tile; ++j) {
-        const int buf = (int)(j & 1u);
-        gload((j + 1) * kBN);
-        tile_step(buf, j, std::false_type{});
-        lstore(buf ^ 1);
-        __syncthreads();
+    // Tile t sits in buffer t & 1.  Full tiles 0..tile-1 need no mask; tile
+    // `tile` holds the diagonal.  The DMA of tile j+1 goes into the buffer
+    // last read before the previous barrier.
+    stage(0, kt0, vt0);
+    publish();
+    uint32_t j = 0;
+    for (; j + 2 <= tile; j += 2) {
+        stage((j + 1) * kBN, kt1, vt1);
+        tile_step(kt0, vt0, j, std::false_type{});
+        publish();
+        stage((j + 2) * kBN, kt0, vt0);
+        tile_step(kt1, vt1, j + 1, std::false_type{});
+        publish();
     }
-    tile_step((int)(tile & 1u), tile, std::true_type{});
+    if (j < tile) {  // j even: tile j in buffer 0, the diagonal tile j + 1 in buffer 1
+        stage((j + 1) * kBN, kt1, vt1);
+        tile_step(kt0, vt0, j, std::false_type{});
+        publish();
+        tile_step(kt1, vt1, tile, std::true_type{});
+    } else {
+        tile_step(kt0, vt0, tile, std::true_type{});
+    }
 
     // ---- epilogue: O = O^T / l, packed [N][Hq][D]
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const float l = l_run[nt] + xor_lane(l_run[nt], 32);
-        const float inv = 1.f / l;
-        const uint32_t query = q0 + 32u * nt + n;
-        if (query >= N) continue;
+    const float l = l_run + xor_lane(l_run, 32);
+    const float inv = 1.f / l;
+    const uint32_t query = q0 + n;
+    if (query < N) {
         f16* orow = a.out + ((uint64_t)query * a.num_heads + head) * kD;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
@@ -303,7 +296,7 @@ __global__ __launch_bounds__(256 * (2 / NT), 1) void prefill_d128(PrefillArgs a)
             for (int i4 = 0; i4 < 4; ++i4) {
                 f16x4 w;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) w[e] = (f16)(o[nt][dt][4 * i4 + e] * inv);
+                for (int e = 0; e < 4; ++e) w[e] = (f16)(o[dt][4 * i4 + e] * inv);
                 *reinterpret_cast<f16x4*>(orow + 32 * dt + 8 * i4 + 4 * hh) = w;
             }
     }
@@ -336,11 +329,7 @@ hipError_t launch_prefill_kernel(const PrefillArgs& a, int path, hipStream_t str
         blocks = (uint64_t)a.q_tiles * quads;
     }
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
-    if (get_option(kOptPrefillWaves) == 4) {
-        hipLaunchKernelGGL(prefill_d128<2>, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
-    } else {
-        hipLaunchKernelGGL(prefill_d128<1>, dim3((uint32_t)blocks), dim3(512), 0, stream, a);
-    }
+    hipLaunchKernelGGL(prefill_d128, dim3((uint32_t)blocks), dim3(kThreads), 0, stream, a);
     return hipGetLastError();
 }
 
