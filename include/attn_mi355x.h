@@ -127,7 +127,9 @@ int attn_prefill_plan(const void* q, const void* k, const void* v, const void* o
 
 /* Process-wide switches for tests and benchmarks (not needed in production):
  * "decode_force_generic", "decode_splits" (0 = automatic),
- * "prefill_force_generic".  Returns 0 or -1 for an unknown name. */
+ * "decode_heads_per_workgroup" (0 = automatic; 1, 2 or 4 KV heads per split
+ * workgroup, at most what Hkv allows), "prefill_force_generic".  Returns 0 or
+ * -1 for an unknown name. */
 int attn_set_option(const char* name, long value);
 
 /* Library build identification (static string). */

@@ -72,6 +72,7 @@ int attn_set_option(const char* name, long value) {
     if (!std::strcmp(name, "decode_force_generic")) which = kOptDecodeForceGeneric;
     else if (!std::strcmp(name, "decode_splits")) which = kOptDecodeSplits;
     else if (!std::strcmp(name, "prefill_force_generic")) which = kOptPrefillForceGeneric;
+    else if (!std::strcmp(name, "decode_heads_per_workgroup")) which = kOptDecodeHeadsPerGroup;
     if (which < 0) return -1;
     g_options[which].store(value, std::memory_order_relaxed);
     return 0;

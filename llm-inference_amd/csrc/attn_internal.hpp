@@ -121,6 +121,7 @@ enum Option {
     kOptDecodeForceGeneric = 0,
     kOptDecodeSplits = 1,        // 0 = automatic
     kOptPrefillForceGeneric = 2,
+    kOptDecodeHeadsPerGroup = 3,  // 0 = automatic; 1, 2 or 4 KV heads per split workgroup
     kOptCount = 8
 };
 long get_option(int which);

@@ -348,7 +348,14 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
                          kv_stride * 2 <= 0x40000000ull && aligned16(q) && aligned16(k) &&
                          aligned16(v) && get_option(kOptDecodeForceGeneric) == 0;
     if (!mfma_ok) return p;
-    const uint32_t hpw = (num_kv_heads % 4 == 0) ? 4 : (num_kv_heads % 2 == 0) ? 2 : 1;
+    // two KV heads per workgroup when Hkv allows: measured fastest at every
+    // SmolLM3 context length (4 heads per workgroup reads whole 1 KiB cache
+    // rows but doubles the merge's partial states; 1 head streams slower)
+    uint32_t hpw = (num_kv_heads % 2 == 0) ? 2 : 1;
+    const long hopt = get_option(kOptDecodeHeadsPerGroup);
+    if (hopt == 4 && num_kv_heads % 4 == 0) hpw = 4;
+    else if (hopt == 2 && num_kv_heads % 2 == 0) hpw = 2;
+    else if (hopt == 1) hpw = 1;
     p.path = hpw == 4 ? 1 : hpw == 2 ? 2 : 3;
     p.block = 512;
     const uint32_t groups = num_kv_heads / hpw;       // grid.y

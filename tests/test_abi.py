@@ -99,7 +99,7 @@ def test_decode_plan_respects_workspace_capacity(attn):
             for L in lengths:
                 for hq, hkv in ((16, 4), (4, 4), (2, 1), (16, 1), (32, 8), (8, 2)):
                     p = attn.decode_plan(L, hq, hkv, 128)
-                    hpw = 4 if hkv % 4 == 0 else 2 if hkv % 2 == 0 else 1
+                    hpw = 2 if hkv % 2 == 0 else 1
                     assert p["path"] == {4: 1, 2: 2, 1: 3}[hpw]
                     assert p["nsplit"] >= 1 and p["chunk"] * p["nsplit"] >= L
                     assert (p["nsplit"] - 1) * p["chunk"] < L  # no empty split
@@ -107,6 +107,13 @@ def test_decode_plan_respects_workspace_capacity(attn):
                     assert hq * p["nstate"] <= hq * ((L + 11) // 12), (splits, L, hq, hkv, p)
     finally:
         attn.set_option("decode_splits", 0)
+    # heads per workgroup can be forced within what Hkv allows
+    try:
+        for hpw, hkv, path in ((4, 4, 1), (4, 2, 2), (2, 4, 2), (1, 4, 3), (4, 1, 3)):
+            attn.set_option("decode_heads_per_workgroup", hpw)
+            assert attn.decode_plan(4096, 16, hkv, 128)["path"] == path, (hpw, hkv)
+    finally:
+        attn.set_option("decode_heads_per_workgroup", 0)
     # head_dim != 128 or an odd stride takes the generic kernel
     assert attn.decode_plan(257, 4, 2, 32)["path"] == 0
     assert attn.decode_plan(257, 4, 2, 128, kv_stride=2 * 128 + 17)["path"] == 0

@@ -129,6 +129,24 @@ def test_decode_independent_of_split_plan(attn, gpu, splits):
     assert_close(got, e, 2e-3, 1e-2, f"splits={splits}")
 
 
+@pytest.mark.parametrize("hpw", [1, 2, 4])
+def test_decode_heads_per_workgroup(attn, gpu, hpw):
+    """Every split-kernel variant (1, 2 or 4 KV heads per workgroup) gives the
+    oracle's result on SmolLM3 shapes."""
+    L = 20001
+    q, k, v = smol_inputs(L, seed=14)
+    e = expected(q, k, v, L)
+    attn.set_option("decode_heads_per_workgroup", hpw)
+    try:
+        plan = attn.decode_plan(L, 16, 4, 128)
+        print(f"[case] decode hpw={hpw} plan={plan}", flush=True)
+        assert plan["path"] == {4: 1, 2: 2, 1: 3}[hpw]
+        got = run_decode(attn, gpu, q, k, v, L, 16, 4, 128)
+    finally:
+        attn.set_option("decode_heads_per_workgroup", 0)
+    assert_close(got, e, 2e-3, 1e-2, f"hpw={hpw}")
+
+
 def test_decode_forced_generic(attn, gpu):
     L = 5000
     q, k, v = smol_inputs(L, seed=10)
@@ -217,10 +235,10 @@ def test_decode_graph_node_update(attn, gpu):
         hipgraph.destroy(graph, exe)
 
 
-@pytest.mark.parametrize("Hq,Hkv", [(16, 2), (8, 1)])
-def test_decode_graph_node_update_other_paths(attn, gpu, Hq, Hkv):
-    """The node patchers re-plan the 2- and 1-KV-head-per-workgroup kernels
-    too (paths 2 and 3): replays equal eager launches bit for bit."""
+@pytest.mark.parametrize("Hq,Hkv,hpw", [(16, 2, 0), (8, 1, 0), (16, 4, 4)])
+def test_decode_graph_node_update_other_paths(attn, gpu, Hq, Hkv, hpw):
+    """The node patchers re-plan every split-kernel variant (4, 2 or 1 KV
+    heads per workgroup): replays equal eager launches bit for bit."""
     import ctypes
 
     from attn_mi355x import hipgraph
@@ -236,7 +254,9 @@ def test_decode_graph_node_update_other_paths(attn, gpu, Hq, Hkv):
     po2, pm2, ps2 = po.clone(), pm.clone(), ps.clone()
     out_g = torch.empty(Hq * D, dtype=torch.float16, device=gpu)
     out_e = torch.empty(Hq * D, dtype=torch.float16, device=gpu)
-    assert attn.decode_plan(Lmax, Hq, Hkv, D)["path"] == (2 if Hkv == 2 else 3)
+    attn.set_option("decode_heads_per_workgroup", hpw)
+    expect_path = 1 if hpw == 4 else (2 if Hkv % 2 == 0 else 3)
+    assert attn.decode_plan(Lmax, Hq, Hkv, D)["path"] == expect_path
     stream = torch.cuda.Stream()
     sp = stream.cuda_stream
     anode, mnode = ctypes.c_void_p(), ctypes.c_void_p()
@@ -262,3 +282,4 @@ def test_decode_graph_node_update_other_paths(attn, gpu, Hq, Hkv):
                          f"graph {Hq}/{Hkv} L={L}")
     finally:
         hipgraph.destroy(graph, exe)
+        attn.set_option("decode_heads_per_workgroup", 0)
