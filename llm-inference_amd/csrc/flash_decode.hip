@@ -7,12 +7,13 @@
 // sqrt(D)) V in fp32, rounded to fp16.
 //
 // Two kernels, as in the reference (attention node + merge node):
-//  * split: grid = (nsplit, Hkv/4).  An 8-wave workgroup owns one contiguous
-//    chunk of keys for 4 KV heads (two waves each), so it reads whole cache
-//    rows, and each wave serves ALL query heads of its group: every K/V byte
-//    is read from HBM exactly once (the reference reads it once per query
-//    head).  Each wave walks its keys in rounds of two 32-key batches whose
-//    32 loads are all issued before the round's first MFMA.
+//  * split: grid = (nsplit, Hkv/HPW).  An 8-wave workgroup owns one
+//    contiguous chunk of keys for HPW KV heads (8/HPW waves each; HPW = 2 by
+//    default, so a workgroup reads 512-byte segments of each cache row), and
+//    each wave serves ALL query heads of its group: every K/V byte is read
+//    from HBM exactly once (the reference reads it once per query head).
+//    Each wave walks its keys in rounds of two 32-key batches whose 32 loads
+//    are all issued before the round's first MFMA.
 //    Scores come from MFMA v_mfma_f32_16x16x32_f16 as S^T = K . Q^T (keys =
 //    rows, the <= 16 grouped query heads = columns): 16-byte K loads are
 //    already in A-operand layout.  The S^T key rows are permuted so that lane
@@ -33,9 +34,11 @@
 //    for 16 output dims of one head: M = max_c m_c, l = sum_c 2^(m_c-M) l_c,
 //    out = sum_c 2^(m_c-M) acc_c / l (an online merge per thread over 16-byte
 //    partial loads, then LDS).
-//    The kernel boundary orders the partial writes before the merge reads;
-//    device-scope atomics/fences inside one kernel were measured to cost far
-//    more on the 8-XCD part than the extra launch.
+//    The kernel boundary orders the partial writes before the merge reads.
+//    An in-kernel merge would need device-scope release/acquire between
+//    workgroups on different XCDs (L2 writeback, counters) and a single
+//    workgroup folding a whole head's partials; measured, it saves less than
+//    the second launch costs.
 #include "attn_internal.hpp"
 
 #include <algorithm>
