@@ -268,14 +268,44 @@ def cpu_baselines(torch, quick):
     qp = torch.randn(1, 4, N, D).to(torch.float16)
     kp = torch.randn(1, 1, N, D).to(torch.float16).repeat_interleave(4, dim=1)
     vp = torch.randn(1, 1, N, D).to(torch.float16).repeat_interleave(4, dim=1)
-    t0 = time.perf_counter()
-    F.scaled_dot_product_attention(qp, kp, vp, is_causal=True)
-    dt = time.perf_counter() - t0
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        F.scaled_dot_product_attention(qp, kp, vp, is_causal=True)
+        times.append(time.perf_counter() - t0)
+    dt = float(np.median(times))
     flops = 2 * 4 * D * N * (N + 1)
     res["torch_prefill"] = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": nthreads,
                             "kind": "reference-pytorch",
                             "sample": f"torch SDPA fp16 causal prefill, N={N}, 4 q heads of one "
-                                      f"KV group (1/4 of C4), {dt:.2f} s"}
+                                      f"KV group (1/4 of C4), median of 3: {dt:.2f} s"}
+    # RoPE as the reference's PyTorch path applies it (python/reference.py:63-73:
+    # fp16 cos/sin, q * cos + rotate_half(q) * sin) on C4's 8192 tokens
+    Nr = 8192
+    pos = torch.arange(Nr, dtype=torch.float32)
+    inv = 1.0 / (THETA ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    ang = torch.outer(pos, inv)
+    cos = torch.cat([ang.cos(), ang.cos()], dim=-1).to(torch.float16)[:, None, :]
+    sin = torch.cat([ang.sin(), ang.sin()], dim=-1).to(torch.float16)[:, None, :]
+    qr = torch.randn(Nr, HQ, D).to(torch.float16)
+    kr = torch.randn(Nr, HKV, D).to(torch.float16)
+
+    def rot(x):
+        x1, x2 = x[..., :D // 2], x[..., D // 2:]
+        return x * cos + torch.cat([-x2, x1], dim=-1) * sin
+
+    rot(qr), rot(kr)
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        rot(qr), rot(kr)
+        times.append(time.perf_counter() - t0)
+    dt = float(np.median(times))
+    res["torch_rope"] = {"value": rope_bytes(Nr) / dt / 1e9, "unit": "GB/s", "cores": nthreads,
+                         "kind": "reference-pytorch",
+                         "sample": f"torch fp16 rotate-half RoPE of Q and K, N={Nr} "
+                                   f"(algorithmic bytes as the fused kernel), median of 5: "
+                                   f"{dt * 1e3:.2f} ms"}
     res["host"] = {"cpu_count": os.cpu_count(), "torch_threads": nthreads,
                    "cpu": platform.processor() or platform.machine(),
                    "torch": torch.__version__}
@@ -419,7 +449,8 @@ def main():
         detail["cpu"] = cpu
         log(f"CPU oracle decode {cpu['oracle']['value']:.2f} GB/s; torch CPU decode "
             f"{cpu['torch_decode']['value']:.2f} GB/s; torch CPU prefill "
-            f"{cpu['torch_prefill']['value']:.3f} TFLOP/s")
+            f"{cpu['torch_prefill']['value']:.3f} TFLOP/s; torch CPU RoPE "
+            f"{cpu['torch_rope']['value']:.1f} GB/s")
 
     traffic = None
     tf = ROOT / "profiles" / "decode_traffic.json"
