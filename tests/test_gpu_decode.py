@@ -283,3 +283,32 @@ def test_decode_graph_node_update_other_paths(attn, gpu, Hq, Hkv, hpw):
     finally:
         hipgraph.destroy(graph, exe)
         attn.set_option("decode_heads_per_workgroup", 0)
+
+
+@pytest.mark.parametrize("L", [100003, 131072])
+def test_decode_long_contexts(attn, gpu, L):
+    """Past C3's longest length, including an odd one: the split plan caps the
+    split count and grows the chunk; still the oracle's result."""
+    q, k, v = smol_inputs(L, seed=15)
+    print(f"[case] decode L={L} plan={attn.decode_plan(L, 16, 4, 128)}", flush=True)
+    got = run_decode(attn, gpu, q, k, v, L, 16, 4, 128)
+    assert_close(got, expected(q, k, v, L), 2e-3, 1e-2, f"L={L}")
+
+
+def test_decode_mfma_padded_kv_stride(attn, gpu):
+    """A padded cache row (kv_stride 576, a multiple of 8) stays on the MFMA
+    split path; rows past L hold sentinels."""
+    L, Hq, Hkv, D, kvs = 5000, 16, 4, 128, 576
+    rng = np.random.default_rng(16)
+    q = rng.standard_normal(Hq * D).astype(np.float16).view(np.uint16)
+    k = np.full((L + 2) * kvs, np.float16(123.0).view(np.uint16), dtype=np.uint16)
+    v = k.copy()
+    for buf in (k, v):
+        rows = buf.reshape(L + 2, kvs)
+        rows[:L, :Hkv * D] = rng.standard_normal((L, Hkv * D)).astype(np.float16).view(np.uint16)
+    plan = attn.decode_plan(L, Hq, Hkv, D, kvs)
+    print(f"[case] decode padded kv_stride={kvs} plan={plan}", flush=True)
+    assert plan["path"] != 0
+    got = run_decode(attn, gpu, q, k, v, L, Hq, Hkv, D, kv_stride=kvs)
+    _, e32 = oracle.attention(q, k, v, 1, Hq, Hkv, D, Hq * D, kvs, L, L - 1, causal=False)
+    assert_close(got, e32.reshape(-1), 2e-3, 1e-2, "padded kv_stride")

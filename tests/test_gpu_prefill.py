@@ -166,3 +166,44 @@ def test_prefill_forced_generic_matches_oracle(attn, gpu):
     finally:
         attn.set_option("prefill_force_generic", 0)
     assert_close(got, oracle_prefill(qkv, cache, N, stride).reshape(-1), 2e-3, 1e-2, "generic")
+
+
+def test_prefill_beyond_c4_odd_length(attn, gpu):
+    """N = 12289 (past C4, not a multiple of the 64-token tile): sampled rows,
+    including the last partial tile, against the fp64 oracle."""
+    N = 12289
+    qkv, cache, stride = engine_inputs(N, seed=31, sigma=0.5)
+    print(f"[case] prefill N={N}", flush=True)
+    got = run_prefill(attn, gpu, qkv, cache, N, stride).reshape(N, -1)
+    rows = np.array([0, 1, 63, 64, 4095, 8191, 8192, 12223, 12224, 12287, 12288])
+    e_rows = oracle_prefill(qkv, cache, N, stride, rows=rows)
+    assert_close(got[rows].reshape(-1), e_rows.reshape(-1), 2e-3, 1e-2, f"N={N}")
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(32, 4), (16, 2)])
+def test_prefill_mfma_group_of_8(attn, gpu, Hq, Hkv):
+    """GQA groups of 8 query heads per KV head take the MFMA path too."""
+    N, D = 300, 128
+    qkv, cache, stride = engine_inputs(N, seed=Hq + Hkv, Hq=Hq, Hkv=Hkv)
+    assert attn.prefill_plan(4096, 4096, 4096, 4096, Hq, Hkv, D, stride, Hkv * D) == 1
+    print(f"[case] prefill Hq={Hq} Hkv={Hkv} N={N}", flush=True)
+    got = run_prefill(attn, gpu, qkv, cache, N, stride, Hq=Hq, Hkv=Hkv)
+    e = oracle_prefill(qkv, cache, N, stride, Hq=Hq, Hkv=Hkv)
+    assert_close(got, e.reshape(-1), 2e-3, 1e-2, f"{Hq}/{Hkv}")
+
+
+def test_prefill_mfma_padded_strides(attn, gpu):
+    """Padded (8-element aligned) Q and K/V row strides stay on the MFMA path."""
+    N, Hq, Hkv, D = 333, 16, 4, 128
+    q_stride, kv_stride = Hq * D + 24, Hkv * D + 8
+    rng = np.random.default_rng(41)
+    q = rng.standard_normal(N * q_stride).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((N + 1) * kv_stride).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((N + 1) * kv_stride).astype(np.float16).view(np.uint16)
+    assert attn.prefill_plan(4096, 4096, 4096, 4096, Hq, Hkv, D, q_stride, kv_stride) == 1
+    print(f"[case] prefill padded strides q={q_stride} kv={kv_stride}", flush=True)
+    out = torch.empty(N * Hq * D, dtype=torch.float16, device=gpu)
+    attn.prefill(dev(q, gpu), dev(k, gpu), dev(v, gpu), out, N, Hq, Hkv, D, q_stride, kv_stride)
+    torch.cuda.synchronize()
+    _, e32 = oracle.attention(q, k, v, N, Hq, Hkv, D, q_stride, kv_stride, N, causal=True)
+    assert_close(host(out), e32.reshape(-1), 2e-3, 1e-2, "padded strides")

@@ -94,6 +94,14 @@ def test_rope_store_kv_decode_position_32768(attn, gpu):
         run_case(attn, gpu, 1, 16, 4, 128, 32768, rotate, True, layers=1, layer=0)
 
 
+def test_rope_store_kv_table_end(attn, gpu):
+    # the last rows of a 131072-position table: a 7-token append ending at
+    # position 131071 (fp32 angles of large positions, bit-exact vs the oracle)
+    for rotate in (True, False):
+        print(f"[case] rope start=131065 rotate={rotate}", flush=True)
+        run_case(attn, gpu, 7, 16, 4, 128, 131065, rotate, True, layers=1, layer=0)
+
+
 def test_launch_rope_in_place(attn, gpu):
     # launch_rope: K rotated in place, no cache (rope.hip.cpp:198-205,
     # test_qkv_gemm.cpp:91-94 interleaved strides)
