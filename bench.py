@@ -60,6 +60,14 @@ def rope_bytes(N, rotate=True):
     return (12544 if rotate else 4096) * N
 
 
+HIDDEN = 2048  # SmolLM3-3B hidden size: the decode QKV projection is 2048 -> QKV
+
+
+def qkv_bytes():
+    """Algorithmic HBM bytes of one decode QKV GEMV: W, x and y once."""
+    return 2 * (QKV * HIDDEN + HIDDEN + QKV)
+
+
 def rand16(torch, n, seed, sigma=1.0, device="cuda"):
     g = torch.Generator(device=device)
     g.manual_seed(seed)
@@ -113,6 +121,40 @@ def bench_decode(torch, A, hipgraph, L, nbuf, steps, warmup, seed=3):
     stream = torch.cuda.Stream()
     ms = time_graph(torch, A, hipgraph, launch, steps, warmup, stream)
     del ks, vs
+    return ms
+
+
+def bench_qkv(torch, A, hipgraph, mode, nbuf, steps, warmup, pos=4000, seed=8):
+    """One decode step's QKV projection over `nbuf` distinct weight matrices
+    in rotation (24 x 12.6 MB exceeds the 256 MB last-level cache, as 36
+    layers' weights do): mode "gemv" (launch_qkv_decode), "fused" (GEMV + RoPE
+    + KV append in one kernel) or "two" (launch_qkv_decode then
+    launch_rope_and_store_kv)."""
+    dev = torch.device("cuda:0")
+    ws = [rand16(torch, QKV * HIDDEN, seed + b, 1.0 / 45) for b in range(nbuf)]
+    x = rand16(torch, HIDDEN, seed - 1)
+    y = torch.empty(QKV, dtype=torch.float16, device=dev)
+    cos, sin = A.rope_tables(pos + 1, D, THETA)
+    dcos, dsin = cos.to(dev), sin.to(dev)
+    cache = torch.empty(2 * (pos + 1) * KV_DIM, dtype=torch.float16, device=dev)
+    kc, vc = cache.data_ptr(), cache.data_ptr() + 2 * (pos + 1) * KV_DIM
+    yp, xp, cp, sp_ = y.data_ptr(), x.data_ptr(), dcos.data_ptr(), dsin.data_ptr()
+    lib = A.lib()
+
+    def launch(i, sp):
+        w = ws[i % nbuf].data_ptr()
+        if mode == "fused":
+            rc = lib.attn_qkv_rope_store_kv_decode(xp, yp, w, kc, vc, cp, sp_, HIDDEN, HQ, HKV, D,
+                                                   pos, 1, sp)
+        else:
+            rc = lib.attn_qkv_decode(xp, yp, w, HIDDEN, QKV, sp)
+            if rc == 0 and mode == "two":
+                rc = lib.attn_rope_store_kv(yp, yp + 2 * Q_DIM, yp + 2 * (Q_DIM + KV_DIM), kc,
+                                            vc, cp, sp_, 1, HQ, HKV, D, QKV, QKV, pos, 1, sp)
+        assert rc == 0
+
+    ms = time_graph(torch, A, hipgraph, launch, steps, warmup, torch.cuda.Stream())
+    del ws
     return ms
 
 
@@ -436,6 +478,14 @@ def main():
             "1": {"us": r1 * 1e3}}
         log(f"rope+append N=8192: {r8k * 1e3:.2f} us ({rope_bytes(8192) / r8k / 1e6:.0f} GB/s); "
             f"N=254 {r254 * 1e3:.2f} us; N=1 {r1 * 1e3:.2f} us")
+        qk = {m: bench_qkv(torch, A, hipgraph, m, 24, steps, warmup)
+              for m in ("gemv", "fused", "two")}
+        detail["qkv_decode"] = {
+            "gemv_us": qk["gemv"] * 1e3, "gemv_GBps": qkv_bytes() / qk["gemv"] / 1e6,
+            "fused_us": qk["fused"] * 1e3, "two_kernel_us": qk["two"] * 1e3}
+        log(f"QKV decode GEMV 2048->3072 cold: {qk['gemv'] * 1e3:.2f} us "
+            f"({qkv_bytes() / qk['gemv'] / 1e6:.0f} GB/s); fused +RoPE+append "
+            f"{qk['fused'] * 1e3:.2f} us vs two launches {qk['two'] * 1e3:.2f} us")
         c5ms, c5b = bench_c5(torch, A, hipgraph, 10)
         detail["c5_36_layer_step"] = {"us": c5ms * 1e3, "bytes": c5b,
                                       "GBps": c5b / c5ms / 1e6,

@@ -103,6 +103,36 @@ int attn_update_merge_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_
  * num_heads * ceil(kv_len / ATTN_KV_CHUNK) (model_inference.hpp:192-198). */
 size_t attn_decode_workspace_states(size_t num_heads, size_t kv_len);
 
+/* launch_qkv_decode (kernels.hpp:38-45; qkv_gemm.hip.cpp:107-116, the GEMV of
+ * matrix_vec_mul.hip.cpp:79-172 with beta = 0): y[total_qkv_dim] =
+ * W[total_qkv_dim][hidden_size] x[hidden_size], fp16 in, fp32 accumulation,
+ * fp16 out; W row-major with the Q rows of all heads, then K, then V.
+ * total_qkv_dim == 0 is a no-op; hidden_size == 0 writes zeros (x, W may then
+ * be null).  Any length and alignment (16-byte loads when hidden_size % 8 == 0
+ * and x, W are 16-byte aligned, element loads otherwise). */
+int attn_qkv_decode(const attn_f16_t* x, attn_f16_t* y, const attn_f16_t* w, size_t hidden_size,
+                    size_t total_qkv_dim, hipStream_t stream);
+
+/* No single counterpart in the reference: launch_qkv_decode followed by
+ * launch_rope_and_store_kv(y, y + Hq*D, y + (Hq+Hkv)*D, k_cache, v_cache, cos,
+ * sin, 1, Hq, Hkv, D, total, total, start_pos, apply_rotation) -- the pair
+ * ModelInference issues back to back in every decode step
+ * (model_inference.hpp:354-369) -- as one kernel.  Results equal that pair's
+ * bit for bit.  For callers that control the decode step (one fewer graph node
+ * and no round trip of Q and K through memory). */
+int attn_qkv_rope_store_kv_decode(const attn_f16_t* x, attn_f16_t* y, const attn_f16_t* w,
+                                  attn_f16_t* k_cache, attn_f16_t* v_cache,
+                                  const attn_f16_t* cos_table, const attn_f16_t* sin_table,
+                                  size_t hidden_size, size_t num_heads, size_t num_kv_heads,
+                                  size_t head_dim, size_t start_pos, int apply_rotation,
+                                  hipStream_t stream);
+
+/* Patches start_pos / apply_rotation of a captured
+ * attn_qkv_rope_store_kv_decode node (as update_rope_and_store_kv_node does for
+ * the RoPE node, rope.hip.cpp:208-241). */
+int attn_update_qkv_rope_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t start_pos,
+                              int apply_rotation);
+
 /* Host-side RoPE tables, fp16 [max_seq_len][head_dim/2]: inv_freq[i] =
  * 1/powf(theta, 2i/D), angle = float(pos)*inv_freq[i], cos/sin in fp32 then
  * RNE to fp16.  Same tables as rope_cache.hpp:48-76 (create_rope_cache minus

@@ -12,6 +12,16 @@
 #include <cstddef>
 #include <hip/hip_runtime.h>
 
+// kernels.hpp:38-45 (fp16 GEMV y = W x; W row-major [total_qkv_dim][hidden])
+void launch_qkv_decode(
+    const __half* d_input_norm,
+    __half* d_qkv_out,
+    const __half* d_qkv_weights,
+    const size_t hidden_size,
+    const size_t total_qkv_dim,
+    hipStream_t stream = nullptr
+);
+
 // kernels.hpp:47-59
 void launch_rope(
     __half* d_q,                 // [seq_len, num_heads, head_dim]
@@ -128,4 +138,33 @@ void update_causal_attention_decode_node(
     hipGraphExec_t graph_exec,
     hipGraphNode_t node,
     size_t kv_cache_len
+);
+
+// Not in the reference: launch_qkv_decode followed by launch_rope_and_store_kv
+// for one decode token (model_inference.hpp:354-369), fused into one kernel
+// with identical results; d_qkv_out receives Q rotated, K and V as projected.
+void launch_qkv_rope_and_store_kv_decode(
+    const __half* d_input_norm,
+    __half* d_qkv_out,
+    const __half* d_qkv_weights,
+    __half* d_k_cache,
+    __half* d_v_cache,
+    const __half* d_cos,
+    const __half* d_sin,
+    size_t hidden_size,
+    size_t num_heads,
+    size_t num_kv_heads,
+    size_t head_dim,
+    size_t start_pos,
+    bool apply_rotation,
+    hipStream_t stream = nullptr
+);
+
+// Not in the reference: patches start_pos / apply_rotation of a captured
+// launch_qkv_rope_and_store_kv_decode node (cf. update_rope_and_store_kv_node).
+void update_qkv_rope_and_store_kv_node(
+    hipGraphExec_t graph_exec,
+    hipGraphNode_t node,
+    size_t start_pos,
+    bool apply_rotation
 );

@@ -161,6 +161,72 @@ int attn_update_rope_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t
     return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
 }
 
+// x and W may be null only for an empty reduction (hidden 0: y = 0).
+static bool qkv_args_ok(const attn_f16_t* x, const attn_f16_t* y, const attn_f16_t* w,
+                        size_t hidden, size_t out_dim) {
+    return y && (hidden == 0 || (x && w)) && fits_u32(out_dim) && fits_u32(hidden) &&
+           fits_u32(out_dim + 1);
+}
+
+int attn_qkv_decode(const attn_f16_t* x, attn_f16_t* y, const attn_f16_t* w, size_t hidden_size,
+                    size_t total_qkv_dim, hipStream_t stream) {
+    if (total_qkv_dim == 0) return 0;  // matrix_vec_mul.hip.cpp:160
+    if (!qkv_args_ok(x, y, w, hidden_size, total_qkv_dim)) return (int)hipErrorInvalidValue;
+    QkvArgs a{};
+    a.x = reinterpret_cast<const f16*>(x);
+    a.w = reinterpret_cast<const f16*>(w);
+    a.y = reinterpret_cast<f16*>(y);
+    a.out_dim = (uint32_t)total_qkv_dim;
+    a.in_dim = (uint32_t)hidden_size;
+    return (int)launch_qkv_kernel(a, false, stream);
+}
+
+int attn_qkv_rope_store_kv_decode(const attn_f16_t* x, attn_f16_t* y, const attn_f16_t* w,
+                                  attn_f16_t* k_cache, attn_f16_t* v_cache,
+                                  const attn_f16_t* cos_table, const attn_f16_t* sin_table,
+                                  size_t hidden_size, size_t num_heads, size_t num_kv_heads,
+                                  size_t head_dim, size_t start_pos, int apply_rotation,
+                                  hipStream_t stream) {
+    const size_t out_dim = (num_heads + 2 * num_kv_heads) * head_dim;
+    if (out_dim == 0) return 0;
+    if (!qkv_args_ok(x, y, w, hidden_size, out_dim)) return (int)hipErrorInvalidValue;
+    if (head_dim & 1u || !k_cache || !v_cache || !cos_table || !sin_table || !fits_u32(start_pos))
+        return (int)hipErrorInvalidValue;
+    QkvArgs a{};
+    a.x = reinterpret_cast<const f16*>(x);
+    a.w = reinterpret_cast<const f16*>(w);
+    a.y = reinterpret_cast<f16*>(y);
+    a.kc = reinterpret_cast<f16*>(k_cache);
+    a.vc = reinterpret_cast<f16*>(v_cache);
+    a.cos_t = reinterpret_cast<const f16*>(cos_table);
+    a.sin_t = reinterpret_cast<const f16*>(sin_table);
+    a.out_dim = (uint32_t)out_dim;
+    a.in_dim = (uint32_t)hidden_size;
+    a.num_heads = (uint32_t)num_heads;
+    a.num_kv_heads = (uint32_t)num_kv_heads;
+    a.head_dim = (uint32_t)head_dim;
+    a.start_pos = (uint32_t)start_pos;
+    a.apply = apply_rotation ? 1u : 0u;
+    return (int)launch_qkv_kernel(a, true, stream);
+}
+
+int attn_update_qkv_rope_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t start_pos,
+                              int apply_rotation) {
+    hipKernelNodeParams params{};
+    hipError_t e = hipGraphKernelNodeGetParams(node, &params);
+    if (e != hipSuccess) return (int)e;
+    if (params.func != qkv_kernel_symbol(true, true) && params.func != qkv_kernel_symbol(true, false))
+        return (int)hipErrorInvalidValue;
+    if (!fits_u32(start_pos)) return (int)hipErrorInvalidValue;
+    QkvArgs a = *reinterpret_cast<const QkvArgs*>(params.kernelParams[0]);
+    a.start_pos = (uint32_t)start_pos;
+    a.apply = apply_rotation ? 1u : 0u;
+    void* args[1] = {&a};
+    params.kernelParams = args;
+    params.extra = nullptr;
+    return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
+}
+
 int attn_prefill_plan(const void* q, const void* k, const void* v, const void* out,
                       size_t num_heads, size_t num_kv_heads, size_t head_dim, size_t q_stride,
                       size_t kv_stride) {

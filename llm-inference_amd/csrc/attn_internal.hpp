@@ -29,6 +29,30 @@ struct RopeArgs {
     uint32_t pad_;
 };
 
+// Decode-step QKV projection y = W x (fp16 in, fp32 accumulate, fp16 out),
+// optionally followed in the same kernel by RoPE + KV-cache append.
+struct QkvArgs {
+    const f16* x;        // [in_dim]
+    const f16* w;        // [out_dim][in_dim] row-major: Q rows, then K, then V
+    f16* y;              // [out_dim] (fused: Q rotated, K and V as projected)
+    f16* kc;             // fused: K cache rows [S][Hkv*D]
+    f16* vc;             // fused: V cache rows
+    const f16* cos_t;    // fused: [S][D/2]
+    const f16* sin_t;
+    uint32_t out_dim;
+    uint32_t in_dim;
+    uint32_t num_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t start_pos;  // fused: cache/table row (patched per decode step)
+    uint32_t apply;      // fused: 1 rotate Q and K, 0 NoPE (patched)
+    uint32_t pad_;
+};
+
+hipError_t launch_qkv_kernel(const QkvArgs& a, bool fused, hipStream_t stream);
+const void* qkv_kernel_symbol(bool fused, bool vec);
+bool qkv_vectorized(const QkvArgs& a);
+
 hipError_t launch_rope_kernel(const RopeArgs& a, bool vector_path, hipStream_t stream);
 bool rope_vector_ok(const RopeArgs& a);
 const void* rope_kernel_symbol(bool vector_path);

@@ -27,6 +27,32 @@ inline void report(int rc) {
 
 }  // namespace
 
+void launch_qkv_decode(const __half* d_input_norm, __half* d_qkv_out,
+                       const __half* d_qkv_weights, const size_t hidden_size,
+                       const size_t total_qkv_dim, hipStream_t stream) {
+    report(attn_qkv_decode(h(d_input_norm), h(d_qkv_out), h(d_qkv_weights), hidden_size,
+                           total_qkv_dim, stream));
+}
+
+void launch_qkv_rope_and_store_kv_decode(const __half* d_input_norm, __half* d_qkv_out,
+                                         const __half* d_qkv_weights, __half* d_k_cache,
+                                         __half* d_v_cache, const __half* d_cos,
+                                         const __half* d_sin, size_t hidden_size,
+                                         size_t num_heads, size_t num_kv_heads, size_t head_dim,
+                                         size_t start_pos, bool apply_rotation,
+                                         hipStream_t stream) {
+    report(attn_qkv_rope_store_kv_decode(h(d_input_norm), h(d_qkv_out), h(d_qkv_weights),
+                                         h(d_k_cache), h(d_v_cache), h(d_cos), h(d_sin),
+                                         hidden_size, num_heads, num_kv_heads, head_dim,
+                                         start_pos, apply_rotation ? 1 : 0, stream));
+}
+
+void update_qkv_rope_and_store_kv_node(hipGraphExec_t graph_exec, hipGraphNode_t node,
+                                       size_t start_pos, bool apply_rotation) {
+    HIP_CHECK((hipError_t)attn_update_qkv_rope_node(graph_exec, node, start_pos,
+                                                    apply_rotation ? 1 : 0));
+}
+
 void launch_rope(__half* d_q, __half* d_k, const __half* d_cos, const __half* d_sin,
                  size_t seq_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
                  size_t q_stride, size_t k_stride, size_t start_pos) {

@@ -53,6 +53,10 @@ def _declare(lib):
         "attn_prefill_plan": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz]),
         "attn_set_option": (_c.c_int, [_c.c_char_p, _c.c_long]),
         "attn_version": (_c.c_char_p, []),
+        "attn_qkv_decode": (_c.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
+        "attn_qkv_rope_store_kv_decode": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
+                                                     _sz, _sz, _sz, _sz, _c.c_int, _vp]),
+        "attn_update_qkv_rope_node": (_c.c_int, [_vp, _vp, _sz, _c.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -76,7 +80,8 @@ def exported_symbols():
     return ["attn_rope_store_kv", "attn_rope", "attn_update_rope_node", "attn_prefill",
             "attn_decode", "attn_update_decode_node", "attn_update_merge_node",
             "attn_decode_workspace_states", "attn_rope_tables", "attn_decode_plan",
-            "attn_prefill_plan", "attn_set_option", "attn_version"]
+            "attn_prefill_plan", "attn_set_option", "attn_version", "attn_qkv_decode",
+            "attn_qkv_rope_store_kv_decode", "attn_update_qkv_rope_node"]
 
 
 def _ptr(x) -> Optional[int]:
@@ -128,6 +133,23 @@ def rope_store_kv(q, k, v, k_cache, v_cache, cos, sin, seq_len, num_heads, num_k
                                   head_dim, q_stride, k_stride, start_pos,
                                   1 if apply_rotation else 0, _stream(stream))
     _check(rc, "attn_rope_store_kv")
+
+
+def qkv_decode(x, y, w, hidden_size, total_qkv_dim, stream=None):
+    """launch_qkv_decode (kernels.hpp:38-45): y = W x, fp16 out."""
+    rc = lib().attn_qkv_decode(_ptr(x), _ptr(y), _ptr(w), hidden_size, total_qkv_dim,
+                               _stream(stream))
+    _check(rc, "attn_qkv_decode")
+
+
+def qkv_rope_store_kv_decode(x, y, w, k_cache, v_cache, cos, sin, hidden_size, num_heads,
+                             num_kv_heads, head_dim, start_pos, apply_rotation, stream=None):
+    """launch_qkv_decode + launch_rope_and_store_kv of one decode step, fused."""
+    rc = lib().attn_qkv_rope_store_kv_decode(_ptr(x), _ptr(y), _ptr(w), _ptr(k_cache),
+                                             _ptr(v_cache), _ptr(cos), _ptr(sin), hidden_size,
+                                             num_heads, num_kv_heads, head_dim, start_pos,
+                                             1 if apply_rotation else 0, _stream(stream))
+    _check(rc, "attn_qkv_rope_store_kv_decode")
 
 
 def rope(q, k, cos, sin, seq_len, num_heads, num_kv_heads, head_dim, q_stride, k_stride,

@@ -33,6 +33,12 @@
  *                                     independent of rows > t).
  *   orc_attention_chunked             equals orc_attention within fp32 error for
  *                                     every chunk size (an unscaled merge fails).
+ *   orc_gemv                          numpy's float64 matrix-vector product (a
+ *                                     library routine) on non-square shapes (a
+ *                                     transposed W fails); identity rows copy x
+ *                                     exactly; the reference's own
+ *                                     test_matrix_vec_mul.cpp inputs (closed
+ *                                     form) within its tolerance of fp64.
  */
 #include <math.h>
 #include <stddef.h>
@@ -360,4 +366,25 @@ void orc_kat_inputs(uint16_t* q, uint16_t* k, uint16_t* v, size_t q_dim, size_t 
             k[t * stride + i] = orc_f32_to_f16(3.f * cosf((float)(t * kv_dim + i + 1) * .13f));
             v[t * stride + i] = orc_f32_to_f16(sinf((float)(t * kv_dim + i + 3) * .19f));
         }
+}
+
+/* ---------------------------------------------------------------- GEMV --- */
+
+/* y[r] = fp16(sum_c W[r][c] * x[c]) for r < out_dim: the beta = 0 GEMV that
+ * launch_qkv_decode runs (qkv_gemm.hip.cpp:107-116 ->
+ * matrix_vec_mul.hip.cpp:79-172).  The reference accumulates fp32 products in
+ * a thread- and lane-dependent order, then rounds the fp32 sum to fp16
+ * (:150).  Here every product of two fp16 values is exact in fp64 and the sum
+ * is carried in fp64, so this is the order-free value the reference's fp32
+ * sum approximates; the fp64 sum is rounded to fp32, then to fp16 (RNE) as in
+ * :150.  A GPU result can differ from it only by the fp32 summation error
+ * around an fp16 rounding boundary (one fp16 ulp in rare elements). */
+void orc_gemv(const uint16_t* w, const uint16_t* x, uint16_t* y, size_t out_dim, size_t in_dim) {
+    for (size_t r = 0; r < out_dim; ++r) {
+        const uint16_t* row = w + r * in_dim;
+        double acc = 0.0;
+        for (size_t c = 0; c < in_dim; ++c)
+            acc += (double)orc_f16_to_f32(row[c]) * (double)orc_f16_to_f32(x[c]);
+        y[r] = orc_f32_to_f16((float)acc);
+    }
 }

@@ -50,6 +50,7 @@ def lib():
         L.orc_kv_total_bytes.restype = _sz
         L.orc_kv_total_bytes.argtypes = [_sz, _sz, _sz, _sz]
         L.orc_kat_inputs.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, _sz]
+        L.orc_gemv.argtypes = [_vp, _vp, _vp, _sz, _sz]
         _lib = L
     return _lib
 
@@ -132,3 +133,30 @@ def kat_inputs(heads, head_dim, kv_heads, length, stride):
     v = np.empty((length + 2) * stride, dtype=np.uint16)
     lib().orc_kat_inputs(_p(q), _p(k), _p(v), q_dim, length, kv_dim, stride)
     return q, k, v
+
+
+def gemv(w, x):
+    """y = fp16(W x) with an fp64 sum (attn_oracle.c:orc_gemv); w uint16 [out][in]."""
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    out_dim, in_dim = w.shape
+    assert x.shape == (in_dim,)
+    y = np.empty(out_dim, dtype=np.uint16)
+    lib().orc_gemv(_p(w), _p(x), _p(y), out_dim, in_dim)
+    return y
+
+
+def qkv_rope_store_kv_decode(w, x, k_cache, v_cache, cos, sin, num_heads, num_kv_heads,
+                             head_dim, start_pos, apply_rotation):
+    """One decode step of model_inference.hpp:354-369: the QKV GEMV, then
+    rope_store_kv on its output (Q rotated in place, K rotated into the cache,
+    V copied).  Returns y; updates the caches in place."""
+    y = gemv(w, x)
+    q_dim, kv_dim = num_heads * head_dim, num_kv_heads * head_dim
+    q = y[:q_dim].copy()
+    k = y[q_dim:q_dim + kv_dim].copy()
+    v = y[q_dim + kv_dim:].copy()
+    rope_store_kv(q, k, v, k_cache, v_cache, cos, sin, 1, num_heads, num_kv_heads, head_dim,
+                  q_dim, kv_dim, start_pos, apply_rotation)
+    y[:q_dim] = q
+    return y

@@ -70,6 +70,10 @@ def test_noop_shapes_touch_nothing(attn):
                               (1, 5, 16, 4, 0), (1, 5, 16, 3, 128)):
         assert lib.attn_decode(None, None, None, None, None, None, None, ql, L, 0, hq, hkv, d, 0,
                                0, None, None, None) == 0
+    # QKV projection with no output rows (matrix_vec_mul.hip.cpp:160)
+    assert lib.attn_qkv_decode(None, None, None, 2048, 0, None) == 0
+    assert lib.attn_qkv_rope_store_kv_decode(None, None, None, None, None, None, None, 2048, 0, 0,
+                                             128, 0, 1, None) == 0
 
 
 def test_invalid_arguments_are_errors(attn):
@@ -86,6 +90,17 @@ def test_invalid_arguments_are_errors(attn):
     assert lib.attn_prefill(None, None, None, None, 8, 16, 4, 128, 0, 0, None) != 0
     assert lib.attn_decode(None, None, None, None, None, None, None, 1, 5, 4, 16, 4, 128, 0, 0,
                            None, None, None) != 0
+    # QKV projection: null output / operands, odd head_dim, missing caches or tables
+    assert lib.attn_qkv_decode(None, None, None, 2048, 3072, None) != 0
+    assert lib.attn_qkv_decode(None, 16, None, 2048, 3072, None) != 0
+    y = 16
+    assert lib.attn_qkv_rope_store_kv_decode(16, y, 16, 16, 16, 16, 16, 2048, 16, 4, 127, 0, 1,
+                                             None) != 0
+    assert lib.attn_qkv_rope_store_kv_decode(16, y, 16, None, 16, 16, 16, 2048, 16, 4, 128, 0, 1,
+                                             None) != 0
+    assert lib.attn_qkv_rope_store_kv_decode(16, y, 16, 16, 16, None, 16, 2048, 16, 4, 128, 0, 1,
+                                             None) != 0
+    assert lib.attn_update_qkv_rope_node(None, None, 0, 1) != 0
 
 
 def test_decode_plan_respects_workspace_capacity(attn):

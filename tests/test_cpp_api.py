@@ -17,8 +17,8 @@ LIB = ROOT / "llm-inference_amd" / "lib" / "libattn_mi355x.so"
 BIN = ROOT / "tests" / "cpp" / "_build" / "test_reference_api"
 HIPCC = "/opt/rocm/bin/hipcc"
 
-# kernels.hpp signatures of the reference (include/kernels/kernels.hpp:47-146),
-# as the C++ demangler prints them
+# kernels.hpp signatures of the reference (include/kernels/kernels.hpp:38-146),
+# plus the fused decode-step producer, as the C++ demangler prints them
 EXPECTED = {
     "launch_rope(__half*, __half*, __half const*, __half const*, unsigned long, unsigned long, "
     "unsigned long, unsigned long, unsigned long, unsigned long, unsigned long)",
@@ -37,6 +37,13 @@ EXPECTED = {
     "hipGraphNode**)",
     "update_merge_attention_decode_node(hipGraphExec*, hipGraphNode*, unsigned long)",
     "update_causal_attention_decode_node(hipGraphExec*, hipGraphNode*, unsigned long)",
+    "launch_qkv_decode(__half const*, __half*, __half const*, unsigned long, unsigned long, "
+    "ihipStream_t*)",
+    # fused decode-step producer (no reference counterpart)
+    "launch_qkv_rope_and_store_kv_decode(__half const*, __half*, __half const*, __half*, __half*, "
+    "__half const*, __half const*, unsigned long, unsigned long, unsigned long, unsigned long, "
+    "unsigned long, bool, ihipStream_t*)",
+    "update_qkv_rope_and_store_kv_node(hipGraphExec*, hipGraphNode*, unsigned long, bool)",
 }
 
 

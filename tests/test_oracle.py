@@ -269,3 +269,48 @@ def test_kv_cache_offsets():
     ko, vo = oracle.kv_offsets(1, S, Hkv, D)
     assert ko == 2 * S * Hkv * D and vo == ko + S * Hkv * D
     assert oracle.kv_total_bytes(36, S, Hkv, D) == 2415992832
+
+# ------------------------------------------------------------------ GEMV ---
+
+
+@pytest.mark.parametrize("out_dim,in_dim", [(37, 2048), (129, 129), (9, 2053), (300, 64),
+                                            (1, 1)])
+def test_gemv_matches_numpy_float64(out_dim, in_dim):
+    # numpy's float64 product is an independent library evaluation; the shapes
+    # are non-square so a transposed W cannot even be formed the same way
+    rng = np.random.default_rng(out_dim * 7 + in_dim)
+    w = (rng.standard_normal((out_dim, in_dim)) / np.sqrt(in_dim)).astype(np.float16)
+    x = rng.standard_normal(in_dim).astype(np.float16)
+    ours = oracle.gemv(w.view(np.uint16), x.view(np.uint16))
+    ref = (w.astype(np.float64) @ x.astype(np.float64)).astype(np.float32).astype(np.float16)
+    d = ulp_diff(ours, ref.view(np.uint16))
+    assert d.max() <= 1 and (d == 0).mean() > 0.999
+
+
+def test_gemv_identity_rows_copy_x():
+    # W = [I; 2I] selects x exactly (and doubles it exactly), an off-by-one in
+    # the row or column index breaks it
+    n = 257
+    x = np.random.default_rng(3).standard_normal(n).astype(np.float16)
+    w = np.concatenate([np.eye(n), 2 * np.eye(n)]).astype(np.float16)
+    y = oracle.gemv(w.view(np.uint16), x.view(np.uint16))
+    assert np.array_equal(y[:n], x.view(np.uint16))
+    assert np.array_equal(f16(y[n:]), (2 * x.astype(np.float32)).astype(np.float16))
+
+
+def gemv_reference_inputs(out_dim, in_dim):
+    """test_matrix_vec_mul.cpp:21-24 closed-form weights and input."""
+    i = np.arange(out_dim * in_dim)
+    w = (((i % 29) - 14) / 64.0).astype(np.float16).reshape(out_dim, in_dim)
+    x = (((np.arange(in_dim) % 17) - 8) / 16.0).astype(np.float16)
+    return w, x
+
+
+@pytest.mark.parametrize("out_dim,in_dim", [(7, 31), (37, 2048), (19, 11008), (9, 2053),
+                                            (3, 0)])
+def test_gemv_reference_known_answers(out_dim, in_dim):
+    # the reference test's own inputs and tolerance (test_matrix_vec_mul.cpp:52-60)
+    w, x = gemv_reference_inputs(out_dim, in_dim)
+    y = f16(oracle.gemv(w.view(np.uint16), x.view(np.uint16))).astype(np.float64)
+    exp = w.astype(np.float64) @ x.astype(np.float64)
+    assert np.all(np.abs(y - exp) <= 1e-3 + 1e-3 * np.abs(exp))
