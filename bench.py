@@ -399,6 +399,24 @@ def profile_workload(torch, A):
         assert rc == 0
     torch.cuda.synchronize()
     log(f"profile: 3 rope+append calls N={N} (algorithmic {rope_bytes(N)} B each)")
+    del qkv, kc, vc, o, cache
+    ws = [rand16(torch, QKV * HIDDEN, 40 + b, 1.0 / 45) for b in range(24)]
+    x = rand16(torch, HIDDEN, 39)
+    y = torch.empty(QKV, dtype=torch.float16, device=dev)
+    kc1 = torch.empty(2 * N * KV_DIM, dtype=torch.float16, device=dev)
+    sp = torch.cuda.current_stream().cuda_stream
+    for i in range(24):
+        assert lib.attn_qkv_decode(x.data_ptr(), y.data_ptr(), ws[i].data_ptr(), HIDDEN, QKV,
+                                   sp) == 0
+    for i in range(24):
+        assert lib.attn_qkv_rope_store_kv_decode(
+            x.data_ptr(), y.data_ptr(), ws[i].data_ptr(), kc1.data_ptr(),
+            kc1.data_ptr() + 2 * N * KV_DIM, dcos.data_ptr(), dsin.data_ptr(), HIDDEN, HQ, HKV,
+            D, N - 1, 1, sp) == 0
+    torch.cuda.synchronize()
+    log(f"profile: 24 + 24 decode QKV calls (GEMV, fused), weights cold "
+        f"(algorithmic {qkv_bytes()} B each)")
+    del ws
     src = torch.empty(128 << 20, dtype=torch.float16, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -416,8 +434,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--profile", action="store_true",
                     help="eager launches only, for rocprofv3 --pmc passes: 16 cold C3 decode "
-                         "calls, 3 C4 prefills, 3 RoPE+append at 8192 tokens and a 256 MiB "
-                         "device copy that calibrates the byte counters")
+                         "calls, 3 C4 prefills, 3 RoPE+append at 8192 tokens, 24 + 24 decode "
+                         "QKV projections (GEMV, fused) and a 256 MiB device copy that "
+                         "calibrates the byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the attention hot path is "
