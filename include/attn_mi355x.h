@@ -133,6 +133,31 @@ int attn_qkv_rope_store_kv_decode(const attn_f16_t* x, attn_f16_t* y, const attn
 int attn_update_qkv_rope_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t start_pos,
                               int apply_rotation);
 
+/* launch_qkv_gemm (kernels.hpp:29-36; qkv_gemm.hip.cpp:7-105, a rocBLAS
+ * gemm_ex with fp32 compute): y[seq_len][total_qkv_dim] =
+ * x[seq_len][hidden_size] . W[total_qkv_dim][hidden_size]^T, fp16 in, fp32
+ * accumulation, fp16 out, all row-major and packed.  seq_len == 0 or
+ * total_qkv_dim == 0 is a no-op; hidden_size == 0 writes zeros (x, W may then
+ * be null).  fp16 MFMA when hidden_size % 64 == 0 and x, W are 16-byte
+ * aligned; any other shape runs a plain fp32-accumulating kernel. */
+int attn_qkv_gemm(const attn_f16_t* x, attn_f16_t* y, const attn_f16_t* w, size_t seq_len,
+                  size_t hidden_size, size_t total_qkv_dim, hipStream_t stream);
+
+/* No single counterpart in the reference: launch_qkv_gemm followed by
+ * launch_rope_and_store_kv(y, y + Hq*D, y + (Hq+Hkv)*D, k_cache, v_cache, cos,
+ * sin, seq_len, Hq, Hkv, D, total, total, start_pos, apply_rotation) -- the
+ * pair ModelInference issues back to back in prefill (model_inference.hpp:
+ * 266-285) -- as one kernel when head_dim == 128, the GEMM takes its MFMA
+ * path and y, the caches and the tables are 16-byte aligned (the two launches
+ * otherwise).  Results equal attn_qkv_gemm followed by
+ * attn_rope_store_kv bit for bit. */
+int attn_qkv_gemm_rope_store_kv(const attn_f16_t* x, attn_f16_t* y, const attn_f16_t* w,
+                                attn_f16_t* k_cache, attn_f16_t* v_cache,
+                                const attn_f16_t* cos_table, const attn_f16_t* sin_table,
+                                size_t seq_len, size_t hidden_size, size_t num_heads,
+                                size_t num_kv_heads, size_t head_dim, size_t start_pos,
+                                int apply_rotation, hipStream_t stream);
+
 /* Host-side RoPE tables, fp16 [max_seq_len][head_dim/2]: inv_freq[i] =
  * 1/powf(theta, 2i/D), angle = float(pos)*inv_freq[i], cos/sin in fp32 then
  * RNE to fp16.  Same tables as rope_cache.hpp:48-76 (create_rope_cache minus
@@ -158,8 +183,10 @@ int attn_prefill_plan(const void* q, const void* k, const void* v, const void* o
 /* Process-wide switches for tests and benchmarks (not needed in production):
  * "decode_force_generic", "decode_splits" (0 = automatic),
  * "decode_heads_per_workgroup" (0 = automatic; 1, 2 or 4 KV heads per split
- * workgroup, at most what Hkv allows), "prefill_force_generic".  Returns 0 or
- * -1 for an unknown name. */
+ * workgroup, at most what Hkv allows), "prefill_force_generic",
+ * "qkv_gemm_force_generic", "qkv_gemm_tokens_per_wave" (0 = automatic; 32, 64
+ * or 128 tokens per wave of the MFMA GEMM).  Returns 0 or -1 for an unknown
+ * name. */
 int attn_set_option(const char* name, long value);
 
 /* Library build identification (static string). */

@@ -12,6 +12,17 @@
 #include <cstddef>
 #include <hip/hip_runtime.h>
 
+// kernels.hpp:29-36 (Y[seq][total] = X[seq][hidden] . W^T; no stream argument:
+// the null stream, as the reference's rocBLAS handle uses)
+void launch_qkv_gemm(
+    const __half* d_input_norm,
+    __half* d_qkv_out,
+    const __half* d_qkv_weights,
+    const size_t seq_len,
+    const size_t hidden_size,
+    const size_t total_qkv_dim
+);
+
 // kernels.hpp:38-45 (fp16 GEMV y = W x; W row-major [total_qkv_dim][hidden])
 void launch_qkv_decode(
     const __half* d_input_norm,
@@ -167,4 +178,25 @@ void update_qkv_rope_and_store_kv_node(
     hipGraphNode_t node,
     size_t start_pos,
     bool apply_rotation
+);
+
+// Not in the reference: launch_qkv_gemm followed by launch_rope_and_store_kv
+// for a prefill of seq_len tokens (model_inference.hpp:266-285), fused into
+// one kernel (head_dim 128) with identical results.
+void launch_qkv_gemm_rope_and_store_kv(
+    const __half* d_input_norm,
+    __half* d_qkv_out,
+    const __half* d_qkv_weights,
+    __half* d_k_cache,
+    __half* d_v_cache,
+    const __half* d_cos,
+    const __half* d_sin,
+    size_t seq_len,
+    size_t hidden_size,
+    size_t num_heads,
+    size_t num_kv_heads,
+    size_t head_dim,
+    size_t start_pos,
+    bool apply_rotation,
+    hipStream_t stream = nullptr
 );

@@ -73,6 +73,8 @@ int attn_set_option(const char* name, long value) {
     else if (!std::strcmp(name, "decode_splits")) which = kOptDecodeSplits;
     else if (!std::strcmp(name, "prefill_force_generic")) which = kOptPrefillForceGeneric;
     else if (!std::strcmp(name, "decode_heads_per_workgroup")) which = kOptDecodeHeadsPerGroup;
+    else if (!std::strcmp(name, "qkv_gemm_force_generic")) which = kOptQkvGemmForceGeneric;
+    else if (!std::strcmp(name, "qkv_gemm_tokens_per_wave")) which = kOptQkvGemmTokensPerWave;
     if (which < 0) return -1;
     g_options[which].store(value, std::memory_order_relaxed);
     return 0;
@@ -225,6 +227,64 @@ int attn_update_qkv_rope_node(hipGraphExec_t graph_exec, hipGraphNode_t node, si
     params.kernelParams = args;
     params.extra = nullptr;
     return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
+}
+
+static int qkv_gemm_args(QkvGemmArgs& a, const attn_f16_t* x, attn_f16_t* y,
+                         const attn_f16_t* w, size_t seq_len, size_t hidden, size_t total) {
+    if (!y || (hidden != 0 && (!x || !w))) return (int)hipErrorInvalidValue;
+    if (!fits_u32(seq_len) || !fits_u32(hidden) || !fits_u32(total + 255))
+        return (int)hipErrorInvalidValue;
+    a = QkvGemmArgs{};
+    a.x = reinterpret_cast<const f16*>(x);
+    a.w = reinterpret_cast<const f16*>(w);
+    a.y = reinterpret_cast<f16*>(y);
+    a.M = (uint32_t)seq_len;
+    a.N = (uint32_t)total;
+    a.K = (uint32_t)hidden;
+    return 0;
+}
+
+int attn_qkv_gemm(const attn_f16_t* x, attn_f16_t* y, const attn_f16_t* w, size_t seq_len,
+                  size_t hidden_size, size_t total_qkv_dim, hipStream_t stream) {
+    if (seq_len == 0 || total_qkv_dim == 0) return 0;
+    QkvGemmArgs a;
+    if (int rc = qkv_gemm_args(a, x, y, w, seq_len, hidden_size, total_qkv_dim)) return rc;
+    return (int)launch_qkv_gemm_kernel(a, false, stream);
+}
+
+int attn_qkv_gemm_rope_store_kv(const attn_f16_t* x, attn_f16_t* y, const attn_f16_t* w,
+                                attn_f16_t* k_cache, attn_f16_t* v_cache,
+                                const attn_f16_t* cos_table, const attn_f16_t* sin_table,
+                                size_t seq_len, size_t hidden_size, size_t num_heads,
+                                size_t num_kv_heads, size_t head_dim, size_t start_pos,
+                                int apply_rotation, hipStream_t stream) {
+    if (seq_len == 0) return 0;
+    const size_t q_dim = num_heads * head_dim, kv_dim = num_kv_heads * head_dim;
+    const size_t total = q_dim + 2 * kv_dim;
+    if (total == 0) return 0;
+    if (head_dim & 1u || !k_cache || !v_cache || !cos_table || !sin_table ||
+        !fits_u32(start_pos + seq_len))
+        return (int)hipErrorInvalidValue;
+    QkvGemmArgs a;
+    if (int rc = qkv_gemm_args(a, x, y, w, seq_len, hidden_size, total)) return rc;
+    const auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+    if (head_dim == 128 && qkv_gemm_mfma_ok(a) && a16(y) && a16(k_cache) && a16(v_cache) &&
+        a16(cos_table) && a16(sin_table)) {
+        a.kc = reinterpret_cast<f16*>(k_cache);
+        a.vc = reinterpret_cast<f16*>(v_cache);
+        a.cos_t = reinterpret_cast<const f16*>(cos_table);
+        a.sin_t = reinterpret_cast<const f16*>(sin_table);
+        a.num_heads = (uint32_t)num_heads;
+        a.num_kv_heads = (uint32_t)num_kv_heads;
+        a.start_pos = (uint32_t)start_pos;
+        a.apply = apply_rotation ? 1u : 0u;
+        return (int)launch_qkv_gemm_kernel(a, true, stream);
+    }
+    // other shapes: the two launches the fused kernel replaces
+    if (hipError_t e = launch_qkv_gemm_kernel(a, false, stream)) return (int)e;
+    return attn_rope_store_kv(y, y + q_dim, y + q_dim + kv_dim, k_cache, v_cache, cos_table,
+                              sin_table, seq_len, num_heads, num_kv_heads, head_dim, total, total,
+                              start_pos, apply_rotation, stream);
 }
 
 int attn_prefill_plan(const void* q, const void* k, const void* v, const void* out,

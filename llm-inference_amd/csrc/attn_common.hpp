@@ -54,4 +54,25 @@ __device__ __forceinline__ float fast_exp2(float x) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// RoPE rotation of 8 pairs (x0[i], x1[i]) = (x[c + i], x[c + D/2 + i]) by
+// (cos, sin) as rope.hip.cpp:44-58 computes it: fp32 products each rounded,
+// no contraction, one fp16 rounding per output.
+__device__ __forceinline__ void rope_rotate8(const f16x8 x0, const f16x8 x1, const f16x8 c,
+                                             const f16x8 s, f16x8& o0, f16x8& o1) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float a = (float)x0[i];
+        const float b = (float)x1[i];
+        const float cc = (float)c[i];
+        const float ss = (float)s[i];
+        const float p0 = a * cc;
+        const float p1 = b * ss;
+        const float p2 = b * cc;
+        const float p3 = a * ss;
+        o0[i] = (f16)(p0 - p1);
+        o1[i] = (f16)(p2 + p3);
+    }
+}
+
 }  // namespace attn

@@ -49,6 +49,34 @@ struct QkvArgs {
     uint32_t pad_;
 };
 
+// Prefill QKV projection Y[M][N] = X[M][K] . W[N][K]^T (fp16 in, fp32
+// accumulate, fp16 out, Y row stride N), optionally followed in the same
+// kernel by RoPE + KV-cache append of the M tokens (D = 128 heads).
+struct QkvGemmArgs {
+    const f16* x;        // [M][K]
+    const f16* w;        // [N][K]: Q rows, then K, then V
+    f16* y;              // [M][N] (fused: Q rotated, K and V as projected)
+    f16* kc;             // fused: K cache rows [S][Hkv*128]
+    f16* vc;             // fused: V cache rows
+    const f16* cos_t;    // fused: [S][64]
+    const f16* sin_t;
+    uint32_t M;
+    uint32_t N;
+    uint32_t K;
+    uint32_t n_tiles;    // set by the launcher
+    uint32_t num_heads;
+    uint32_t num_kv_heads;
+    uint32_t start_pos;  // fused: cache/table row of token 0
+    uint32_t apply;      // fused: 1 rotate Q and K, 0 NoPE
+    uint32_t vec_out;    // set by the launcher: 16-byte stores of y (N % 8 == 0, y aligned)
+    uint32_t pad_;
+};
+
+bool qkv_gemm_mfma_ok(const QkvGemmArgs& a);
+int qkv_gemm_wmt(uint32_t M);
+// fused: only when qkv_gemm_mfma_ok (hipErrorInvalidValue otherwise)
+hipError_t launch_qkv_gemm_kernel(const QkvGemmArgs& a, bool fused, hipStream_t stream);
+
 hipError_t launch_qkv_kernel(const QkvArgs& a, bool fused, hipStream_t stream);
 const void* qkv_kernel_symbol(bool fused, bool vec);
 bool qkv_vectorized(const QkvArgs& a);
@@ -146,6 +174,8 @@ enum Option {
     kOptDecodeSplits = 1,        // 0 = automatic
     kOptPrefillForceGeneric = 2,
     kOptDecodeHeadsPerGroup = 3,  // 0 = automatic; 1, 2 or 4 KV heads per split workgroup
+    kOptQkvGemmForceGeneric = 4,
+    kOptQkvGemmTokensPerWave = 5, // 0 = automatic; 32, 64 or 128
     kOptCount = 8
 };
 long get_option(int which);

@@ -27,6 +27,26 @@ inline void report(int rc) {
 
 }  // namespace
 
+void launch_qkv_gemm(const __half* d_input_norm, __half* d_qkv_out,
+                     const __half* d_qkv_weights, const size_t seq_len,
+                     const size_t hidden_size, const size_t total_qkv_dim) {
+    report(attn_qkv_gemm(h(d_input_norm), h(d_qkv_out), h(d_qkv_weights), seq_len, hidden_size,
+                         total_qkv_dim, nullptr));
+}
+
+void launch_qkv_gemm_rope_and_store_kv(const __half* d_input_norm, __half* d_qkv_out,
+                                       const __half* d_qkv_weights, __half* d_k_cache,
+                                       __half* d_v_cache, const __half* d_cos,
+                                       const __half* d_sin, size_t seq_len, size_t hidden_size,
+                                       size_t num_heads, size_t num_kv_heads, size_t head_dim,
+                                       size_t start_pos, bool apply_rotation,
+                                       hipStream_t stream) {
+    report(attn_qkv_gemm_rope_store_kv(h(d_input_norm), h(d_qkv_out), h(d_qkv_weights),
+                                       h(d_k_cache), h(d_v_cache), h(d_cos), h(d_sin), seq_len,
+                                       hidden_size, num_heads, num_kv_heads, head_dim, start_pos,
+                                       apply_rotation ? 1 : 0, stream));
+}
+
 void launch_qkv_decode(const __half* d_input_norm, __half* d_qkv_out,
                        const __half* d_qkv_weights, const size_t hidden_size,
                        const size_t total_qkv_dim, hipStream_t stream) {

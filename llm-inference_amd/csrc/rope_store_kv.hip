@@ -21,24 +21,6 @@ namespace attn {
 
 namespace {
 
-__device__ __forceinline__ void rotate8(const f16x8 x0, const f16x8 x1, const f16x8 c,
-                                        const f16x8 s, f16x8& o0, f16x8& o1) {
-#pragma clang fp contract(off)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float a = (float)x0[i];
-        const float b = (float)x1[i];
-        const float cc = (float)c[i];
-        const float ss = (float)s[i];
-        const float p0 = a * cc;
-        const float p1 = b * ss;
-        const float p2 = b * cc;
-        const float p3 = a * ss;
-        o0[i] = (f16)(p0 - p1);
-        o1[i] = (f16)(p2 + p3);
-    }
-}
-
 __global__ __launch_bounds__(256) void rope_store_kv_vec(RopeArgs a) {
     const uint32_t lanes = a.lanes_per_head;
     const uint32_t slots = a.num_heads + 2u * a.num_kv_heads;
@@ -62,7 +44,7 @@ __global__ __launch_bounds__(256) void rope_store_kv_vec(RopeArgs a) {
         const f16x8 c = ld16(a.cos_t + pos * half + off0);
         const f16x8 s = ld16(a.sin_t + pos * half + off0);
         f16x8 o0, o1;
-        rotate8(ld16(x + off0), ld16(x + off1), c, s, o0, o1);
+        rope_rotate8(ld16(x + off0), ld16(x + off1), c, s, o0, o1);
         st16(x + off0, o0);
         st16(x + off1, o1);
         return;
@@ -75,7 +57,7 @@ __global__ __launch_bounds__(256) void rope_store_kv_vec(RopeArgs a) {
             const f16x8 c = ld16(a.cos_t + pos * half + off0);
             const f16x8 s = ld16(a.sin_t + pos * half + off0);
             f16x8 o0, o1;
-            rotate8(ld16(src + off0), ld16(src + off1), c, s, o0, o1);
+            rope_rotate8(ld16(src + off0), ld16(src + off1), c, s, o0, o1);
             st16(dst + off0, o0);
             st16(dst + off1, o1);
         } else {

@@ -57,6 +57,8 @@ def _declare(lib):
         "attn_qkv_rope_store_kv_decode": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                                      _sz, _sz, _sz, _sz, _c.c_int, _vp]),
         "attn_update_qkv_rope_node": (_c.c_int, [_vp, _vp, _sz, _c.c_int]),
+        "attn_qkv_gemm": (_c.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+        "attn_qkv_gemm_rope_store_kv": (_c.c_int, [_vp] * 7 + [_sz] * 6 + [_c.c_int, _vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -81,7 +83,8 @@ def exported_symbols():
             "attn_decode", "attn_update_decode_node", "attn_update_merge_node",
             "attn_decode_workspace_states", "attn_rope_tables", "attn_decode_plan",
             "attn_prefill_plan", "attn_set_option", "attn_version", "attn_qkv_decode",
-            "attn_qkv_rope_store_kv_decode", "attn_update_qkv_rope_node"]
+            "attn_qkv_rope_store_kv_decode", "attn_update_qkv_rope_node", "attn_qkv_gemm",
+            "attn_qkv_gemm_rope_store_kv"]
 
 
 def _ptr(x) -> Optional[int]:
@@ -150,6 +153,24 @@ def qkv_rope_store_kv_decode(x, y, w, k_cache, v_cache, cos, sin, hidden_size, n
                                              num_heads, num_kv_heads, head_dim, start_pos,
                                              1 if apply_rotation else 0, _stream(stream))
     _check(rc, "attn_qkv_rope_store_kv_decode")
+
+
+def qkv_gemm(x, y, w, seq_len, hidden_size, total_qkv_dim, stream=None):
+    """launch_qkv_gemm (kernels.hpp:29-36): y[seq][total] = x[seq][hidden] . W^T."""
+    rc = lib().attn_qkv_gemm(_ptr(x), _ptr(y), _ptr(w), seq_len, hidden_size, total_qkv_dim,
+                             _stream(stream))
+    _check(rc, "attn_qkv_gemm")
+
+
+def qkv_gemm_rope_store_kv(x, y, w, k_cache, v_cache, cos, sin, seq_len, hidden_size, num_heads,
+                           num_kv_heads, head_dim, start_pos, apply_rotation, stream=None):
+    """launch_qkv_gemm + launch_rope_and_store_kv of a prefill, fused."""
+    rc = lib().attn_qkv_gemm_rope_store_kv(_ptr(x), _ptr(y), _ptr(w), _ptr(k_cache),
+                                           _ptr(v_cache), _ptr(cos), _ptr(sin), seq_len,
+                                           hidden_size, num_heads, num_kv_heads, head_dim,
+                                           start_pos, 1 if apply_rotation else 0,
+                                           _stream(stream))
+    _check(rc, "attn_qkv_gemm_rope_store_kv")
 
 
 def rope(q, k, cos, sin, seq_len, num_heads, num_kv_heads, head_dim, q_stride, k_stride,

@@ -33,7 +33,7 @@
  *                                     independent of rows > t).
  *   orc_attention_chunked             equals orc_attention within fp32 error for
  *                                     every chunk size (an unscaled merge fails).
- *   orc_gemv                          numpy's float64 matrix-vector product (a
+ *   orc_gemv, orc_gemm                numpy's float64 matrix-vector product (a
  *                                     library routine) on non-square shapes (a
  *                                     transposed W fails); identity rows copy x
  *                                     exactly; the reference's own
@@ -43,6 +43,7 @@
 #include <math.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* ---------------------------------------------------------------- fp16 --- */
@@ -387,4 +388,32 @@ void orc_gemv(const uint16_t* w, const uint16_t* x, uint16_t* y, size_t out_dim,
             acc += (double)orc_f16_to_f32(row[c]) * (double)orc_f16_to_f32(x[c]);
         y[r] = orc_f32_to_f16((float)acc);
     }
+}
+
+/* y[m][n] = fp16(sum_k x[m][k] * w[n][k]) for m < rows, n < out_dim: the
+ * prefill QKV projection of launch_qkv_gemm (qkv_gemm.hip.cpp:7-105, rocBLAS
+ * gemm_ex with fp32 compute and fp16 output), row by row as orc_gemv: exact
+ * fp16 products, fp64 sum, rounded to fp32 then fp16. */
+void orc_gemm(const uint16_t* x, const uint16_t* w, uint16_t* y, size_t rows, size_t out_dim,
+              size_t in_dim) {
+    /* the same arithmetic as orc_gemv per row, with W and each x row widened
+     * once instead of per product */
+    double* wd = (double*)malloc(sizeof(double) * (out_dim * in_dim + in_dim + 1));
+    if (!wd) {
+        for (size_t m = 0; m < rows; ++m)
+            orc_gemv(w, x + m * in_dim, y + m * out_dim, out_dim, in_dim);
+        return;
+    }
+    double* xd = wd + out_dim * in_dim;
+    for (size_t i = 0; i < out_dim * in_dim; ++i) wd[i] = (double)orc_f16_to_f32(w[i]);
+    for (size_t m = 0; m < rows; ++m) {
+        for (size_t c = 0; c < in_dim; ++c) xd[c] = (double)orc_f16_to_f32(x[m * in_dim + c]);
+        for (size_t r = 0; r < out_dim; ++r) {
+            const double* row = wd + r * in_dim;
+            double acc = 0.0;
+            for (size_t c = 0; c < in_dim; ++c) acc += row[c] * xd[c];
+            y[m * out_dim + r] = orc_f32_to_f16((float)acc);
+        }
+    }
+    free(wd);
 }

@@ -51,6 +51,7 @@ def lib():
         L.orc_kv_total_bytes.argtypes = [_sz, _sz, _sz, _sz]
         L.orc_kat_inputs.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, _sz]
         L.orc_gemv.argtypes = [_vp, _vp, _vp, _sz, _sz]
+        L.orc_gemm.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz]
         _lib = L
     return _lib
 
@@ -143,6 +144,19 @@ def gemv(w, x):
     assert x.shape == (in_dim,)
     y = np.empty(out_dim, dtype=np.uint16)
     lib().orc_gemv(_p(w), _p(x), _p(y), out_dim, in_dim)
+    return y
+
+
+def gemm(x, w):
+    """y[m] = fp16(W x[m]) with fp64 sums (attn_oracle.c:orc_gemm); x uint16
+    [rows][in], w uint16 [out][in]."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    rows, in_dim = x.shape
+    out_dim = w.shape[0]
+    assert w.shape == (out_dim, in_dim)
+    y = np.empty((rows, out_dim), dtype=np.uint16)
+    lib().orc_gemm(_p(x), _p(w), _p(y), rows, out_dim, in_dim)
     return y
 
 

@@ -39,6 +39,11 @@ EXPECTED = {
     "update_causal_attention_decode_node(hipGraphExec*, hipGraphNode*, unsigned long)",
     "launch_qkv_decode(__half const*, __half*, __half const*, unsigned long, unsigned long, "
     "ihipStream_t*)",
+    "launch_qkv_gemm(__half const*, __half*, __half const*, unsigned long, unsigned long, "
+    "unsigned long)",
+    "launch_qkv_gemm_rope_and_store_kv(__half const*, __half*, __half const*, __half*, __half*, "
+    "__half const*, __half const*, unsigned long, unsigned long, unsigned long, unsigned long, "
+    "unsigned long, unsigned long, bool, ihipStream_t*)",
     # fused decode-step producer (no reference counterpart)
     "launch_qkv_rope_and_store_kv_decode(__half const*, __half*, __half const*, __half*, __half*, "
     "__half const*, __half const*, unsigned long, unsigned long, unsigned long, unsigned long, "

@@ -314,3 +314,18 @@ def test_gemv_reference_known_answers(out_dim, in_dim):
     y = f16(oracle.gemv(w.view(np.uint16), x.view(np.uint16))).astype(np.float64)
     exp = w.astype(np.float64) @ x.astype(np.float64)
     assert np.all(np.abs(y - exp) <= 1e-3 + 1e-3 * np.abs(exp))
+
+
+def test_gemm_rows_match_gemv_and_numpy():
+    # orc_gemm is orc_gemv per token row; against numpy float64 on a
+    # non-square product (a transposed operand has the wrong shape)
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((37, 96)).astype(np.float16)
+    w = (rng.standard_normal((50, 96)) / 10).astype(np.float16)
+    y = oracle.gemm(x.view(np.uint16), w.view(np.uint16))
+    assert y.shape == (37, 50)
+    for m in (0, 17, 36):
+        assert np.array_equal(y[m], oracle.gemv(w.view(np.uint16), x[m].view(np.uint16)))
+    ref = (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32).astype(np.float16)
+    d = ulp_diff(y, ref.view(np.uint16))
+    assert d.max() <= 1 and (d == 0).mean() > 0.999
