@@ -115,11 +115,13 @@ def test_qkv_gemm_smollm3_8192(attn, gpu):
 
 
 @pytest.mark.parametrize("tokens_per_wave", [32, 64, 128])
-def test_qkv_gemm_tile_variants_identical(attn, gpu, tokens_per_wave):
-    """Every tile shape sums each output in the same k order, so the three
-    variants give the same bits (and match the oracle)."""
-    M = 700
-    x, w = rand_inputs(M, TOTAL, HIDDEN, 5)
+@pytest.mark.parametrize("M,N", [(700, TOTAL), (1100, 1280)])
+def test_qkv_gemm_tile_variants_identical(attn, gpu, tokens_per_wave, M, N):
+    """Every tile shape (64, 128 or 256 tokens x 128 features) sums each
+    output in the same k order, so all variants give the same bits (and match
+    the oracle)."""
+    print(f"[case] gemm variants M={M} N={N} tpw={tokens_per_wave}", flush=True)
+    x, w = rand_inputs(M, N, HIDDEN, 5)
     base = run_gemm(attn, gpu, x, w)
     try:
         attn.set_option("qkv_gemm_tokens_per_wave", tokens_per_wave)
@@ -163,7 +165,8 @@ def fused_case(attn, device, M, start_pos, rotate, Hq=HQ, Hkv=HKV, Dh=D, K=HIDDE
 
 
 @pytest.mark.parametrize("M,start_pos,rotate", [(254, 0, True), (254, 0, False), (1000, 37, True),
-                                                (3000, 5, True), (64, 32700, False)])
+                                                (3000, 5, True), (64, 32700, False),
+                                                (8192, 0, True), (4100, 9, False)])
 def test_qkv_gemm_rope_store_kv_fused_bitexact(attn, gpu, M, start_pos, rotate):
     """Fused == launch_qkv_gemm + launch_rope_and_store_kv bit for bit in Y
     and every cache element; the oracle's RoPE applied to the GPU GEMM output
