@@ -158,6 +158,46 @@ def bench_qkv(torch, A, hipgraph, mode, nbuf, steps, warmup, pos=4000, seed=8):
     return ms
 
 
+def bench_qkv_prefill(torch, A, M, mode, steps, warmup, seed=9, trials=3):
+    """Prefill QKV projection of M tokens (2048 -> 3072), ms per call: mode
+    "gemm" (launch_qkv_gemm), "fused" (GEMM + RoPE + KV append in one kernel)
+    or "two" (launch_qkv_gemm then launch_rope_and_store_kv)."""
+    dev = torch.device("cuda:0")
+    x = rand16(torch, M * HIDDEN, seed)
+    w = rand16(torch, QKV * HIDDEN, seed + 1, 1.0 / 45)
+    y = torch.empty(M * QKV, dtype=torch.float16, device=dev)
+    cos, sin = A.rope_tables(M, D, THETA)
+    dcos, dsin = cos.to(dev), sin.to(dev)
+    cache = torch.empty(2 * M * KV_DIM, dtype=torch.float16, device=dev)
+    kc, vc = cache.data_ptr(), cache.data_ptr() + 2 * M * KV_DIM
+    yp = y.data_ptr()
+
+    def call():
+        if mode == "fused":
+            A.qkv_gemm_rope_store_kv(x, y, w, kc, vc, dcos, dsin, M, HIDDEN, HQ, HKV, D, 0, True)
+        else:
+            A.qkv_gemm(x, y, w, M, HIDDEN, QKV)
+            if mode == "two":
+                A.rope_store_kv(yp, yp + 2 * Q_DIM, yp + 2 * (Q_DIM + KV_DIM), kc, vc, dcos, dsin,
+                                M, HQ, HKV, D, QKV, QKV, 0, True)
+
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(trials):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) / steps)
+    return best
+
+
 def bench_prefill(torch, A, N, steps, warmup, seed=4, sigma=0.5, trials=3):
     """Prefill ms per call: `warmup` untimed calls (the clock ramps for tens of
     calls under MFMA load), then the best of `trials` timed runs of `steps`."""
@@ -417,6 +457,17 @@ def profile_workload(torch, A):
     log(f"profile: 24 + 24 decode QKV calls (GEMV, fused), weights cold "
         f"(algorithmic {qkv_bytes()} B each)")
     del ws
+    xp = rand16(torch, N * HIDDEN, 38)
+    wp = rand16(torch, QKV * HIDDEN, 37, 1.0 / 45)
+    yq = torch.empty(N * QKV, dtype=torch.float16, device=dev)
+    for _ in range(3):
+        A.qkv_gemm(xp, yq, wp, N, HIDDEN, QKV)
+    for _ in range(3):
+        A.qkv_gemm_rope_store_kv(xp, yq, wp, kc1, kc1.data_ptr() + 2 * N * KV_DIM, dcos, dsin, N,
+                                 HIDDEN, HQ, HKV, D, 0, True)
+    torch.cuda.synchronize()
+    log(f"profile: 3 + 3 prefill QKV calls N={N} (GEMM, fused; {2 * N * QKV * HIDDEN} FLOP each)")
+    del xp, wp, yq
     src = torch.empty(128 << 20, dtype=torch.float16, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -435,8 +486,9 @@ def main():
     ap.add_argument("--profile", action="store_true",
                     help="eager launches only, for rocprofv3 --pmc passes: 16 cold C3 decode "
                          "calls, 3 C4 prefills, 3 RoPE+append at 8192 tokens, 24 + 24 decode "
-                         "QKV projections (GEMV, fused) and a 256 MiB device copy that "
-                         "calibrates the byte counters")
+                         "QKV projections (GEMV, fused), 3 + 3 prefill QKV projections at 8192 "
+                         "tokens (GEMM, fused) and a 256 MiB device copy that calibrates the "
+                         "byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the attention hot path is "
@@ -505,6 +557,16 @@ def main():
         log(f"QKV decode GEMV 2048->3072 cold: {qk['gemv'] * 1e3:.2f} us "
             f"({qkv_bytes() / qk['gemv'] / 1e6:.0f} GB/s); fused +RoPE+append "
             f"{qk['fused'] * 1e3:.2f} us vs two launches {qk['two'] * 1e3:.2f} us")
+        qp = {}
+        for Mq in (8192, 254):
+            r = {m: bench_qkv_prefill(torch, A, Mq, m, 20, 20) for m in ("gemm", "fused", "two")}
+            fl = 2 * Mq * QKV * HIDDEN
+            qp[str(Mq)] = {"gemm_us": r["gemm"] * 1e3, "gemm_TFLOPs": fl / r["gemm"] / 1e9,
+                           "fused_us": r["fused"] * 1e3, "two_kernel_us": r["two"] * 1e3}
+            log(f"QKV prefill GEMM {Mq}x2048->3072: {r['gemm'] * 1e3:.1f} us "
+                f"({fl / r['gemm'] / 1e9:.0f} TFLOP/s); fused +RoPE+append {r['fused'] * 1e3:.1f} us "
+                f"vs two launches {r['two'] * 1e3:.1f} us")
+        detail["qkv_prefill"] = qp
         c5ms, c5b = bench_c5(torch, A, hipgraph, 10)
         detail["c5_36_layer_step"] = {"us": c5ms * 1e3, "bytes": c5b,
                                       "GBps": c5b / c5ms / 1e6,
