@@ -10,6 +10,13 @@
 //      (cache rows past L hold 123, output guards -123, interleaved Q stride).
 //   4. A graph-captured decode step over several layers with per-step node
 //      patching, model_inference.hpp:96-134, compared with eager launches.
+//   5. launch_qkv_decode on the shapes, closed-form inputs, guards and
+//      tolerance of tests/test_matrix_vec_mul.cpp:8-70 (beta = 0).
+//   6. A graph-captured decode step built on the fused
+//      launch_qkv_rope_and_store_kv_decode (patched per token) against eager
+//      launch_qkv_decode + launch_rope_and_store_kv + decode, bit for bit.
+//   7. launch_qkv_gemm against an fp64 CPU product, and the fused
+//      launch_qkv_gemm_rope_and_store_kv against the two launches, bit for bit.
 // Prints one PASS/FAIL line per test; exit status is the number of failures.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -413,6 +420,218 @@ void test_graph_decode_step() {
     report("graph_decode_step_node_patching", all);
 }
 
+// ---------------------------------------------------------------- test 5
+void test_qkv_decode_reference_gemv() {
+    struct Shape { size_t out_dim, in_dim, offset; };
+    const Shape shapes[] = {{1, 1, 0},     {7, 31, 0},    {129, 129, 0}, {37, 2048, 0},
+                            {19, 11008, 0}, {22016, 2048, 0}, {2048, 2048, 0}, {3072, 2048, 0},
+                            {3, 0, 0},     {7, 8, 0},     {9, 2053, 0},  {5, 2056, 0},
+                            {7, 4096, 0},  {5, 2056, 1}};
+    hipStream_t stream;
+    HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+    bool all = true;
+    char detail[128] = "";
+    for (const Shape& sh : shapes) {
+        std::vector<__half> w(sh.out_dim * sh.in_dim + sh.offset + 1), x(sh.in_dim + sh.offset + 1);
+        for (size_t i = 0; i < sh.out_dim * sh.in_dim; ++i)
+            w[sh.offset + i] = __float2half((float)((int)(i % 29) - 14) / 64.0f);
+        for (size_t i = 0; i < sh.in_dim; ++i)
+            x[sh.offset + i] = __float2half((float)((int)(i % 17) - 8) / 16.0f);
+        std::vector<__half> y(sh.out_dim + 2, __float2half(NAN));
+        y.front() = y.back() = __float2half(123.0f);
+        __half *dw = upload(w), *dx = upload(x), *dy = upload(y);
+        launch_qkv_decode(dx + sh.offset, dy + 1, dw + sh.offset, sh.in_dim, sh.out_dim, stream);
+        HIP_CHECK(hipGetLastError());
+        HIP_CHECK(hipStreamSynchronize(stream));
+        const auto got = download(dy, y.size());
+        bool ok = __half2float(got.front()) == 123.0f && __half2float(got.back()) == 123.0f;
+        for (size_t r = 0; r < sh.out_dim; ++r) {
+            double e = 0.0;
+            for (size_t c = 0; c < sh.in_dim; ++c)
+                e += (double)__half2float(w[sh.offset + r * sh.in_dim + c]) *
+                     __half2float(x[sh.offset + c]);
+            const float a = __half2float(got[r + 1]);
+            if (!std::isfinite(a) || std::fabs(a - e) > 1e-3 + 1e-3 * std::fabs(e)) ok = false;
+        }
+        if (!ok) {
+            std::snprintf(detail, sizeof detail, "out=%zu in=%zu offset=%zu", sh.out_dim,
+                          sh.in_dim, sh.offset);
+            all = false;
+        }
+        for (void* p : {(void*)dw, (void*)dx, (void*)dy}) HIP_CHECK(hipFree(p));
+    }
+    // no rows: nothing launched, null pointers untouched
+    launch_qkv_decode(nullptr, nullptr, nullptr, 2048, 0);
+    HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipStreamDestroy(stream));
+    report("qkv_decode_reference_gemv_shapes", all, detail);
+}
+
+// ---------------------------------------------------------------- test 6
+void test_graph_fused_qkv_decode_step() {
+    const size_t layers = 4, heads = 16, kv_heads = 4, head_dim = 128, hidden = 2048;
+    const size_t q_dim = heads * head_dim, kv_dim = kv_heads * head_dim, total = q_dim + 2 * kv_dim;
+    const size_t prompt = 200, steps = 4;
+    Config cfg{layers, prompt + steps + 1, kv_heads, head_dim};
+    KVCache graph_cache(cfg), eager_cache(cfg);
+    RopeCache rope = create_rope_cache(cfg.max_seq_len, head_dim, 5.0e6f);
+    std::mt19937 gen(11);
+    std::normal_distribution<float> nd;
+    std::vector<__half> cache_init(cfg.num_layers * 2 * cfg.max_seq_len * kv_dim);
+    for (auto& v : cache_init) v = __float2half(nd(gen));
+    HIP_CHECK(hipMemcpy(graph_cache.get_k_cache(0), cache_init.data(), cache_init.size() * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(eager_cache.get_k_cache(0), cache_init.data(), cache_init.size() * 2, hipMemcpyHostToDevice));
+    std::vector<__half> wts(layers * total * hidden);
+    for (auto& v : wts) v = __float2half(nd(gen) / 45.0f);
+    __half* d_w = upload(wts);
+    std::vector<std::vector<__half>> x_steps(steps, std::vector<__half>(hidden));
+    for (auto& st : x_steps)
+        for (auto& v : st) v = __float2half(nd(gen));
+    __half *d_x, *y_g, *y_e, *out_g, *out_e;
+    HIP_CHECK(hipMalloc(&d_x, hidden * 2));
+    HIP_CHECK(hipMalloc(&y_g, layers * total * 2));
+    HIP_CHECK(hipMalloc(&y_e, layers * total * 2));
+    HIP_CHECK(hipMalloc(&out_g, layers * q_dim * 2));
+    HIP_CHECK(hipMalloc(&out_e, layers * q_dim * 2));
+    const size_t cap = heads * ((cfg.max_seq_len + KV_CHUNK - 1) / KV_CHUNK);
+    float *po, *pm, *ps;
+    HIP_CHECK(hipMalloc(&po, cap * head_dim * 4));
+    HIP_CHECK(hipMalloc(&pm, cap * 4));
+    HIP_CHECK(hipMalloc(&ps, cap * 4));
+    hipStream_t stream;
+    HIP_CHECK(hipStreamCreate(&stream));
+    struct Nodes { hipGraphNode_t store_kv, attention, merge; };
+    std::vector<Nodes> nodes(layers);
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    // graph: the fused producer (model_inference.hpp:354-369 as one launch)
+    auto enqueue_fused = [&](size_t start_pos) {
+        for (size_t l = 0; l < layers; ++l) {
+            __half* a = y_g + l * total;
+            launch_qkv_rope_and_store_kv_decode(d_x, a, d_w + l * total * hidden,
+                                                graph_cache.get_k_cache(l),
+                                                graph_cache.get_v_cache(l), rope.d_cos,
+                                                rope.d_sin, hidden, heads, kv_heads, head_dim,
+                                                start_pos, (l + 1) % 4 != 0, stream);
+            nodes[l].store_kv = last_captured_node(stream);
+            launch_causal_attention_decode_vectorized(
+                a, graph_cache.get_k_cache(l), graph_cache.get_v_cache(l), out_g + l * q_dim, po,
+                pm, ps, 1, start_pos + 1, start_pos, heads, kv_heads, head_dim, total, kv_dim,
+                stream, &nodes[l].attention, &nodes[l].merge);
+        }
+    };
+    // eager: the reference's two launches
+    auto enqueue_two = [&](size_t start_pos) {
+        for (size_t l = 0; l < layers; ++l) {
+            __half* a = y_e + l * total;
+            launch_qkv_decode(d_x, a, d_w + l * total * hidden, hidden, total, stream);
+            launch_rope_and_store_kv(a, a + q_dim, a + q_dim + kv_dim, eager_cache.get_k_cache(l),
+                                     eager_cache.get_v_cache(l), rope.d_cos, rope.d_sin, 1,
+                                     heads, kv_heads, head_dim, total, total, start_pos,
+                                     (l + 1) % 4 != 0, stream);
+            launch_causal_attention_decode_vectorized(
+                a, eager_cache.get_k_cache(l), eager_cache.get_v_cache(l), out_e + l * q_dim, po,
+                pm, ps, 1, start_pos + 1, start_pos, heads, kv_heads, head_dim, total, kv_dim,
+                stream, nullptr, nullptr);
+        }
+    };
+    bool all = true;
+    for (size_t step = 0; step < steps; ++step) {
+        const size_t start_pos = prompt + step;
+        HIP_CHECK(hipMemcpy(d_x, x_steps[step].data(), hidden * 2, hipMemcpyHostToDevice));
+        if (!exec) {
+            HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeGlobal));
+            enqueue_fused(start_pos);
+            HIP_CHECK(hipStreamEndCapture(stream, &graph));
+            HIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+        } else {
+            for (size_t l = 0; l < layers; ++l) {
+                update_qkv_rope_and_store_kv_node(exec, nodes[l].store_kv, start_pos,
+                                                  (l + 1) % 4 != 0);
+                update_causal_attention_decode_node(exec, nodes[l].attention, start_pos + 1);
+                update_merge_attention_decode_node(exec, nodes[l].merge, start_pos + 1);
+            }
+        }
+        HIP_CHECK(hipGraphLaunch(exec, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        enqueue_two(start_pos);
+        HIP_CHECK(hipStreamSynchronize(stream));
+        const auto og = download(out_g, layers * q_dim), oe = download(out_e, layers * q_dim);
+        const auto yg = download(y_g, layers * total), ye = download(y_e, layers * total);
+        const auto cg = download(graph_cache.get_k_cache(0), cache_init.size());
+        const auto ce = download(eager_cache.get_k_cache(0), cache_init.size());
+        if (!(same_bits(og.data(), oe.data(), og.size()) && same_bits(yg.data(), ye.data(), yg.size()) &&
+              same_bits(cg.data(), ce.data(), cg.size()))) {
+            std::printf("  fused graph / two-launch mismatch at step %zu\n", step);
+            all = false;
+        }
+    }
+    HIP_CHECK(hipGraphExecDestroy(exec));
+    HIP_CHECK(hipGraphDestroy(graph));
+    HIP_CHECK(hipStreamDestroy(stream));
+    for (void* p : {(void*)d_w, (void*)d_x, (void*)y_g, (void*)y_e, (void*)out_g, (void*)out_e,
+                    (void*)po, (void*)pm, (void*)ps})
+        HIP_CHECK(hipFree(p));
+    report("graph_fused_qkv_decode_step", all);
+}
+
+// ---------------------------------------------------------------- test 7
+void test_qkv_gemm_prefill() {
+    const size_t heads = 16, kv_heads = 4, head_dim = 128, hidden = 2048, tokens = 70;
+    const size_t q_dim = heads * head_dim, kv_dim = kv_heads * head_dim, total = q_dim + 2 * kv_dim;
+    Config cfg{2, tokens + 8, kv_heads, head_dim};
+    KVCache fused_cache(cfg), two_cache(cfg);
+    const size_t cache_bytes = cfg.num_layers * 2 * cfg.max_seq_len * kv_dim * 2;
+    HIP_CHECK(hipMemset(fused_cache.get_k_cache(0), 0, cache_bytes));
+    HIP_CHECK(hipMemset(two_cache.get_k_cache(0), 0, cache_bytes));
+    RopeCache rope = create_rope_cache(cfg.max_seq_len, head_dim, 5.0e6f);
+    std::mt19937 gen(21);
+    std::normal_distribution<float> nd;
+    std::vector<__half> x(tokens * hidden), w(total * hidden);
+    for (auto& v : x) v = __float2half(nd(gen));
+    for (auto& v : w) v = __float2half(nd(gen) / 45.0f);
+    __half *dx = upload(x), *dw = upload(w), *y1, *y2;
+    HIP_CHECK(hipMalloc(&y1, tokens * total * 2));
+    HIP_CHECK(hipMalloc(&y2, tokens * total * 2));
+    // the GEMM against an fp64 CPU product (null stream, as the reference)
+    launch_qkv_gemm(dx, y1, dw, tokens, hidden, total);
+    HIP_CHECK(hipDeviceSynchronize());
+    const auto got = download(y1, tokens * total);
+    std::vector<double> wd(w.size());
+    for (size_t i = 0; i < w.size(); ++i) wd[i] = __half2float(w[i]);
+    bool gemm_ok = true;
+    for (size_t m = 0; m < tokens; ++m)
+        for (size_t r = 0; r < total; ++r) {
+            double e = 0.0;
+            for (size_t c = 0; c < hidden; ++c) e += wd[r * hidden + c] * __half2float(x[m * hidden + c]);
+            const float a = __half2float(got[m * total + r]);
+            if (!std::isfinite(a) || std::fabs(a - e) > 2e-3 + 1e-2 * std::fabs(e)) gemm_ok = false;
+        }
+    report("qkv_gemm_vs_fp64", gemm_ok);
+    // fused projection + RoPE + append against the two launches, layer 1 with
+    // rotation at start_pos 5, layer 0 NoPE at 0
+    bool fused_ok = true;
+    for (size_t l = 0; l < 2; ++l) {
+        const size_t start = l == 1 ? 5 : 0;
+        const bool apply = l == 1;
+        launch_qkv_gemm_rope_and_store_kv(dx, y1, dw, fused_cache.get_k_cache(l),
+                                          fused_cache.get_v_cache(l), rope.d_cos, rope.d_sin,
+                                          tokens, hidden, heads, kv_heads, head_dim, start, apply);
+        launch_qkv_gemm(dx, y2, dw, tokens, hidden, total);
+        launch_rope_and_store_kv(y2, y2 + q_dim, y2 + q_dim + kv_dim, two_cache.get_k_cache(l),
+                                 two_cache.get_v_cache(l), rope.d_cos, rope.d_sin, tokens, heads,
+                                 kv_heads, head_dim, total, total, start, apply);
+        HIP_CHECK(hipDeviceSynchronize());
+        const auto a = download(y1, tokens * total), b = download(y2, tokens * total);
+        const auto ca = download(fused_cache.get_k_cache(l), 2 * cfg.max_seq_len * kv_dim);
+        const auto cb = download(two_cache.get_k_cache(l), 2 * cfg.max_seq_len * kv_dim);
+        if (!same_bits(a.data(), b.data(), a.size()) || !same_bits(ca.data(), cb.data(), ca.size()))
+            fused_ok = false;
+    }
+    report("qkv_gemm_fused_rope_store_kv_bitexact", fused_ok);
+    for (void* p : {(void*)dx, (void*)dw, (void*)y1, (void*)y2}) HIP_CHECK(hipFree(p));
+}
+
 }  // namespace
 
 int main() {
@@ -422,6 +641,9 @@ int main() {
     test_rope_and_store_kv();
     test_decode_vs_prefill_rows();
     test_graph_decode_step();
+    test_qkv_decode_reference_gemv();
+    test_graph_fused_qkv_decode_step();
+    test_qkv_gemm_prefill();
     std::printf("%d failure(s)\n", g_failures);
     return g_failures;
 }

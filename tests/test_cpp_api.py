@@ -96,5 +96,5 @@ def test_cpp_reference_api_program(gpu):
     print(r.stdout)
     print(r.stderr)
     lines = [l for l in r.stdout.splitlines() if l.startswith(("PASS", "FAIL"))]
-    assert len(lines) == 4, r.stdout + r.stderr
+    assert len(lines) == 8, r.stdout + r.stderr
     assert r.returncode == 0, r.stdout + r.stderr
