@@ -242,10 +242,13 @@ def bench_rope(torch, A, hipgraph, N, nbuf, steps, warmup, rotate=True, seed=6):
     return time_graph(torch, A, hipgraph, launch, steps, warmup, stream)
 
 
-def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769):
+def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769, producer="rope"):
     """36-layer attention-only decode step: per layer RoPE(+append) of one new
     token at position L-1 (NoPE on every 4th layer, model_inference.hpp:358)
-    and Flash-Decode over L keys, captured as one 72-node graph."""
+    and Flash-Decode over L keys, captured as one 72-node graph.  producer
+    "qkv_fused" / "qkv_two" start each layer from a hidden vector instead:
+    the QKV GEMV (2048 -> 3072, per-layer weights) fused with the RoPE/append
+    (72 nodes) or as the reference's two launches (108 nodes)."""
     dev = torch.device("cuda:0")
     S = L
     cache = torch.empty(layers * 2 * S * KV_DIM, dtype=torch.float16, device=dev)
@@ -265,14 +268,29 @@ def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769):
     sp = stream.cuda_stream
     start_pos = L - 1
 
+    if producer != "rope":
+        ws = rand16(torch, layers * QKV * HIDDEN, 600, 1.0 / 45)
+        x = rand16(torch, HIDDEN, 599)
+
     def enqueue():
         for l in range(layers):
             s = qkv[l].data_ptr()
             kc = cb + 2 * (l * 2 * S * KV_DIM)
             vc = kc + 2 * S * KV_DIM
-            rc = lib.attn_rope_store_kv(s, s + 2 * Q_DIM, s + 2 * (Q_DIM + KV_DIM), kc, vc,
-                                        dcos.data_ptr(), dsin.data_ptr(), 1, HQ, HKV, D, QKV,
-                                        QKV, start_pos, 1 if (l + 1) % 4 != 0 else 0, sp)
+            apply = 1 if (l + 1) % 4 != 0 else 0
+            if producer == "qkv_fused":
+                rc = lib.attn_qkv_rope_store_kv_decode(
+                    x.data_ptr(), s, ws.data_ptr() + 2 * l * QKV * HIDDEN, kc, vc,
+                    dcos.data_ptr(), dsin.data_ptr(), HIDDEN, HQ, HKV, D, start_pos, apply, sp)
+            else:
+                rc = 0
+                if producer == "qkv_two":
+                    rc = lib.attn_qkv_decode(x.data_ptr(), s, ws.data_ptr() + 2 * l * QKV * HIDDEN,
+                                             HIDDEN, QKV, sp)
+                if rc == 0:
+                    rc = lib.attn_rope_store_kv(s, s + 2 * Q_DIM, s + 2 * (Q_DIM + KV_DIM), kc,
+                                                vc, dcos.data_ptr(), dsin.data_ptr(), 1, HQ, HKV,
+                                                D, QKV, QKV, start_pos, apply, sp)
             assert rc == 0
             rc = lib.attn_decode(s, kc, vc, out[l].data_ptr(), po.data_ptr(), pm.data_ptr(),
                                  ps.data_ptr(), 1, L, start_pos, HQ, HKV, D, QKV, KV_DIM, sp,
@@ -296,6 +314,9 @@ def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769):
     ms = e0.elapsed_time(e1) / replays
     nrot = sum(1 for l in range(layers) if (l + 1) % 4 != 0)
     byts = layers * decode_bytes(L) + nrot * rope_bytes(1, True) + (layers - nrot) * rope_bytes(1, False)
+    if producer != "rope":
+        byts += layers * qkv_bytes()
+        del ws
     del cache
     return ms, byts
 
@@ -572,6 +593,11 @@ def main():
                                       "GBps": c5b / c5ms / 1e6,
                                       "pct_of_hbm_peak": 100 * c5b / c5ms / 1e6 / PEAK_HBM_GBS}
         log(f"C5 36-layer decode step: {c5ms * 1e3:.1f} us ({c5b / c5ms / 1e6:.0f} GB/s)")
+        c5q = {p: bench_c5(torch, A, hipgraph, 10, producer=p) for p in ("qkv_fused", "qkv_two")}
+        detail["c5_with_qkv_projection"] = {
+            p: {"us": v[0] * 1e3, "bytes": v[1], "GBps": v[1] / v[0] / 1e6} for p, v in c5q.items()}
+        log(f"C5 with the QKV projection: fused producer {c5q['qkv_fused'][0] * 1e3:.1f} us, "
+            f"GEMV + RoPE {c5q['qkv_two'][0] * 1e3:.1f} us")
 
     cpu = None
     if not args.no_cpu:
