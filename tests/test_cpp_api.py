@@ -89,6 +89,32 @@ def test_reference_headers_compile(tmp_path):
     assert r.returncode == 0, r.stderr
 
 
+@pytest.mark.parametrize("call", [
+    "update_rope_and_store_kv_node(nullptr, nullptr, 5, true)",
+    "update_causal_attention_decode_node(nullptr, nullptr, 5)",
+    "update_merge_attention_decode_node(nullptr, nullptr, 5)",
+    "update_qkv_rope_and_store_kv_node(nullptr, nullptr, 5, true)",
+])
+def test_node_updaters_exit_through_hip_check(tmp_path, call):
+    """The reference's updaters wrap hipGraphExecKernelNodeSetParams in
+    HIP_CHECK (causal_attention.hip.cpp:975-1026, rope.hip.cpp:208-241): a
+    failure prints the HIP error and exits with status 1.  A node that cannot
+    be read (here a null node, on any machine) takes that path."""
+    src = tmp_path / "updater_failure.cpp"
+    src.write_text('#include "kernels/kernels.hpp"\n#include <cstdio>\n'
+                   f"int main() {{ {call}; std::puts(\"returned\"); return 0; }}\n")
+    exe = tmp_path / "updater_failure"
+    lib_dir = ROOT / "llm-inference_amd" / "lib"
+    r = subprocess.run([HIPCC, "-std=c++17", "-I", str(ROOT / "include"), str(src), "-o", str(exe),
+                        "-L", str(lib_dir), "-lattn_mi355x", f"-Wl,-rpath,{lib_dir}"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1, (r.returncode, r.stdout, r.stderr)
+    assert "returned" not in r.stdout
+    assert "[HIP Error]" in r.stderr
+
+
 @pytest.mark.gpu
 def test_cpp_reference_api_program(gpu):
     assert BIN.exists(), f"{BIN} not built: run __graft_entry__.build()"
