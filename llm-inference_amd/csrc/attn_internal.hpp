@@ -69,7 +69,7 @@ struct QkvGemmArgs {
     uint32_t start_pos;  // fused: cache/table row of token 0
     uint32_t apply;      // fused: 1 rotate Q and K, 0 NoPE
     uint32_t vec_out;    // set by the launcher: 16-byte stores of y (N % 8 == 0, y aligned)
-    uint32_t pad_;
+    uint32_t m_tiles;    // set by the launcher: token tiles
 };
 
 bool qkv_gemm_mfma_ok(const QkvGemmArgs& a);

@@ -80,10 +80,22 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)reinterpret_cast<uintptr_t>((LDS_AS const char*)(LDS_AS const void*)p);
 }
 
-// blockIdx -> (token tile, feature tile)
-__device__ __forceinline__ void map_tile(uint32_t bid, uint32_t n_tiles, uint32_t& mt,
-                                         uint32_t& nt) {
-    if ((n_tiles & 7u) == 0) {
+// blockIdx -> (token tile, feature tile).  Workgroups are dispatched
+// round-robin over the 8 XCDs (bid % 8), each with its own L2.  When the tile
+// grid splits 2 x 4, XCD x owns token half x / 4 and feature quarter x % 4
+// (SmolLM3 at 8192 tokens: 16 token tiles x 6 feature tiles, 16 MB of X and
+// 3 MB of W per XCD, so W stays in L2 and each X tile is fetched once per
+// XCD); otherwise, when the feature tiles divide by 8, XCD x owns feature
+// tiles x, x + 8, ... and walks all token tiles.
+__device__ __forceinline__ void map_tile(uint32_t bid, uint32_t m_tiles, uint32_t n_tiles,
+                                         uint32_t& mt, uint32_t& nt) {
+    if ((m_tiles & 1u) == 0 && (n_tiles & 3u) == 0) {
+        const uint32_t xcd = bid & 7u, j = bid >> 3;
+        const uint32_t nm = m_tiles >> 1, nn = n_tiles >> 2;
+        const uint32_t ml = j / nn;
+        mt = (xcd >> 2) * nm + ml;
+        nt = (xcd & 3u) * nn + (j - ml * nn);
+    } else if ((n_tiles & 7u) == 0) {
         const uint32_t per = n_tiles >> 3;
         const uint32_t xcd = bid & 7u, j = bid >> 3;
         mt = j / per;
@@ -120,7 +132,7 @@ __global__ __launch_bounds__(kThreads, 1) void qkv_gemm_mfma(QkvGemmArgs a) {
     const uint32_t n = (uint32_t)lane & 31u, hh = (uint32_t)lane >> 5;
 
     uint32_t m_tile, n_tile;
-    map_tile(blockIdx.x, a.n_tiles, m_tile, n_tile);
+    map_tile(blockIdx.x, a.m_tiles, a.n_tiles, m_tile, n_tile);
     // uniform by construction; keeps the buffer resources in SGPRs
     m_tile = __builtin_amdgcn_readfirstlane(m_tile);
     n_tile = __builtin_amdgcn_readfirstlane(n_tile);
@@ -347,6 +359,7 @@ hipError_t launch_mfma(const QkvGemmArgs& a, bool fused, hipStream_t stream) {
     const uint64_t m_tiles = (a.M + BM - 1u) / BM;
     const uint64_t blocks = m_tiles * b.n_tiles;
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
+    b.m_tiles = (uint32_t)m_tiles;
     if (fused)
         hipLaunchKernelGGL((qkv_gemm_mfma<WMT, true>), dim3((uint32_t)blocks), dim3(kThreads), 0,
                            stream, b);
