@@ -23,9 +23,9 @@
 //    (16 rows x 16 B per pass) hit 16 distinct bank groups; the DMA source of
 //    each lane is chosen to produce that order.  Rows past M or N read as zero
 //    through the buffer range check.
-//  * Workgroups are dispatched round-robin over the 8 XCDs; when the feature
-//    tiles divide by 8, each XCD owns N/1024 feature tiles (their W rows stay
-//    in its L2) and walks the token tiles.
+//  * Workgroups are dispatched round-robin over the 8 XCDs; the tile grid is
+//    split over them (2 x 4 when it divides: each XCD owns half the token
+//    tiles and a quarter of the feature tiles, whose W rows stay in its L2).
 //  * Epilogue: fp32 -> fp16 (the GEMM's output rounding), then for the fused
 //    kernel the rope.hip.cpp:44-58 rotation on those fp16 values (fp32
 //    products each rounded, no contraction): Q rows written rotated, K rows
