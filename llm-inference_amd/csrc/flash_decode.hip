@@ -30,10 +30,10 @@
 //    K/V are read through raw buffer resources covering exactly the chunk:
 //    rows past the chunk read as zero without a memory access, so the last
 //    batch needs no clamping and the prefetch past the end is free.
-//  * merge: grid = (Hq, D/16).  Each workgroup folds every split's partial
-//    for 16 output dims of one head: M = max_c m_c, l = sum_c 2^(m_c-M) l_c,
-//    out = sum_c 2^(m_c-M) acc_c / l (an online merge per thread over 16-byte
-//    partial loads, then LDS).
+//  * merge: grid = (Hq, D/4), one wave per workgroup.  Each wave folds
+//    every split's partial for 4 output dims of one head: M = max_c m_c,
+//    l = sum_c 2^(m_c-M) l_c, out = sum_c 2^(m_c-M) acc_c / l (an online merge
+//    per lane over 16-byte partial loads, then xor shuffles).
 //    The kernel boundary orders the partial writes before the merge reads.
 //    An in-kernel merge would need device-scope release/acquire between
 //    workgroups on different XCDs (L2 writeback, counters) and a single
@@ -225,14 +225,8 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     }
 }
 
-// grid (Hq, D/16), 256 threads.  Thread (sl, q4) = (t / 4, t % 4) folds the
-// partials of splits c = sl, sl + 64, ... for dims d0 + 4q4 .. +3 with an
-// online merge; the 64 split lanes then meet in LDS.  All loads go through
-// range-checked buffer resources sized to this head's S partials, so splits
-// past S read as zero without branches (their maxima are replaced by -inf).
-constexpr int kMergeDims = 16;
-constexpr int kMergeLanes = 64;  // split lanes per workgroup
-constexpr int kMergeRound = 4;   // splits per thread per round of loads
+constexpr int kMergeDims = 4;    // output dims per merge workgroup (one wave)
+constexpr int kMergeRound = 4;   // splits per lane per round of loads
 
 __device__ __forceinline__ float buf_ldf(BufRsrc r, uint32_t byte_off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 0));
@@ -241,40 +235,36 @@ __device__ __forceinline__ f32x4 buf_ldf4(BufRsrc r, uint32_t byte_off) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
 }
 
-__global__ __launch_bounds__(256) void flash_decode_merge(DecodeArgs a) {
-    __shared__ float s_m[kMergeLanes];
-    __shared__ float s_l[kMergeLanes];
-    __shared__ float s_w[kMergeLanes];
-    __shared__ float s_a[kMergeLanes][kMergeDims + 1];
-    __shared__ float s_num[256 / kMergeDims][kMergeDims];
-    __shared__ float s_den;
-    const uint32_t t = threadIdx.x;
+// grid (Hq, D/4), one wave per workgroup.  Lane j folds the partials of
+// splits j, j + 64, ... for 4 output dims of one head with an online merge
+// (all loads of a round issued first, through range-checked buffer
+// resources: splits past nstate read as zero and get weight 0); the 64 lanes
+// then combine with xor shuffles -- no LDS, no barrier.
+__global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
+    const uint32_t lane = threadIdx.x;
     const uint32_t h = blockIdx.x;
     const uint32_t d0 = blockIdx.y * kMergeDims;
-    const uint32_t q4 = t & 3u;
-    const uint32_t sl = t >> 2;
     const uint32_t S = a.nstate;
     const BufRsrc rpm = make_rsrc(a.part_max + (uint64_t)h * S, S * 4u);
     const BufRsrc rps = make_rsrc(a.part_sum + (uint64_t)h * S, S * 4u);
     const BufRsrc rpo = make_rsrc(a.part_out + (uint64_t)h * S * kD, S * kD * 4u);
-    const uint32_t dbyte = (d0 + 4u * q4) * 4u;
+    const uint32_t dbyte = d0 * 4u;
 
     float m = -INFINITY, l = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    // all loads of a round are issued before the fold (one round for S <= 256)
-    for (uint32_t base = sl; base < S; base += kMergeLanes * kMergeRound) {
+    for (uint32_t base = lane; base < S; base += 64u * kMergeRound) {
         float mc[kMergeRound], lc[kMergeRound];
         f32x4 ac[kMergeRound];
 #pragma unroll
         for (int u = 0; u < kMergeRound; ++u) {
-            const uint32_t c = base + (uint32_t)(kMergeLanes * u);
+            const uint32_t c = base + 64u * (uint32_t)u;
             mc[u] = buf_ldf(rpm, c * 4u);
             lc[u] = buf_ldf(rps, c * 4u);
             ac[u] = buf_ldf4(rpo, c * (kD * 4u) + dbyte);
         }
 #pragma unroll
         for (int u = 0; u < kMergeRound; ++u)
-            if (base + (uint32_t)(kMergeLanes * u) >= S) mc[u] = -INFINITY;
+            if (base + 64u * (uint32_t)u >= S) mc[u] = -INFINITY;
         float mn = m;
 #pragma unroll
         for (int u = 0; u < kMergeRound; ++u) mn = fmaxf(mn, mc[u]);  // split `base` is valid
@@ -289,42 +279,25 @@ __global__ __launch_bounds__(256) void flash_decode_merge(DecodeArgs a) {
         }
         m = mn;
     }
-    if (q4 == 0) {
-        s_m[sl] = m;  // lanes without splits: -inf, weight 0 below
-        s_l[sl] = l;
+    // lanes without splits hold m = -inf and get weight 0
+    float mx = m;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, xor_lane(mx, o));
+    const float w = fast_exp2(m - mx);
+    float den = w * l;
+    f32x4 num = acc * w;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        den += xor_lane(den, o);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) num[e] += xor_lane(num[e], o);
     }
+    // every lane holds the sums; lane e writes dim d0 + e (out may be 2-byte aligned)
+    if (lane < (uint32_t)kMergeDims) {
+        float v = num[0];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s_a[sl][4 * q4 + e] = acc[e];
-    __syncthreads();
-    if (t < kMergeLanes) {  // wave 0: global max, weights, denominator
-        const float mi = s_m[t];
-        float mx = mi;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, xor_lane(mx, o));
-        const float w = fast_exp2(mi - mx);
-        s_w[t] = w;
-        float den = w * s_l[t];
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) den += xor_lane(den, o);
-        if (t == 0) s_den = den;
-    }
-    __syncthreads();
-    {
-        const uint32_t dd = t % kMergeDims, grp = t / kMergeDims;  // 16 groups x 4 lanes
-        float num = 0.f;
-#pragma unroll
-        for (int k = 0; k < kMergeLanes / (256 / kMergeDims); ++k) {
-            const uint32_t i = grp * (kMergeLanes / (256 / kMergeDims)) + k;
-            num += s_w[i] * s_a[i][dd];
-        }
-        s_num[grp][dd] = num;
-    }
-    __syncthreads();
-    if (t < kMergeDims) {
-        float tot = 0.f;
-#pragma unroll
-        for (int g2 = 0; g2 < 256 / kMergeDims; ++g2) tot += s_num[g2][t];
-        a.out[(uint64_t)h * kD + d0 + t] = (f16)(tot / s_den);
+        for (int e = 1; e < 4; ++e) v = lane == (uint32_t)e ? num[e] : v;
+        a.out[(uint64_t)h * kD + d0 + lane] = (f16)(v / den);
     }
 }
 
@@ -404,7 +377,7 @@ hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStre
 }
 
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(flash_decode_merge, dim3(a.num_heads, kD / kMergeDims), dim3(256), 0,
+    hipLaunchKernelGGL(flash_decode_merge, dim3(a.num_heads, kD / kMergeDims), dim3(64), 0,
                        stream, a);
     return hipGetLastError();
 }
