@@ -12,7 +12,7 @@
 //  * K and V of a 64-key tile are staged in LDS once per workgroup and shared
 //    by the 4 heads (the reference re-reads them per head), copied straight
 //    from global memory into LDS by buffer_load ... lds (no VGPRs, no LDS
-//    stores).  Rows are padded (K 272 B, V 288 B) so the MFMA operand reads
+//    stores).  Rows are padded (K 272 B, V 320 B) so the MFMA operand reads
 //    are free of bank conflicts; a DMA instruction writes 1 KiB of LDS and
 //    the lanes that land on padding fetch a harmless copy of a row's first
 //    16 bytes.  Rows past N read as zero through the buffer range check.
@@ -43,11 +43,14 @@ constexpr int kBN = 64;        // keys per tile
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kKP = kD + 8;    // K row pitch (halves): conflict-free 16 B A-operand reads
-constexpr int kVP = kD + 16;   // V row pitch (halves): conflict-free transposing reads
+// V row pitch (halves): 320-byte rows start 16 banks apart, so the 4 rows x
+// 64 bytes that 32 lanes of a transposing read address cover the 64 banks
+// once (288-byte rows overlapped by 8 banks: 2-way conflicts)
+constexpr int kVP = kD + 32;
 constexpr int kKChunks = kKP / 8;             // 16-byte LDS chunks per K row (17)
-constexpr int kVChunks = kVP / 8;             // ... per V row (18)
+constexpr int kVChunks = kVP / 8;             // ... per V row (20)
 constexpr int kKDma = kBN * kKChunks / 64;    // 1 KiB DMA instructions per K tile (17)
-constexpr int kVDma = kBN * kVChunks / 64;    // ... per V tile (18)
+constexpr int kVDma = kBN * kVChunks / 64;    // ... per V tile (20)
 constexpr int kDmaPerWave = (kVDma + kWaves - 1) / kWaves;  // 3
 
 #define LDS_AS __attribute__((address_space(3)))
