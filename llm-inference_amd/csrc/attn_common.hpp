@@ -41,6 +41,41 @@ __device__ __forceinline__ f16x8 buf_ld16(BufRsrc r, uint32_t byte_off) {
     return __builtin_bit_cast(f16x8, v);
 }
 
+// One LDS-DMA instruction (buffer_load_dwordx4 ... lds): each lane copies 16
+// bytes at byte offset voff of the buffer described by `r` to LDS bytes
+// [lds + 16 lane, lds + 16 lane + 16).  Issued as inline assembly so that the
+// compiler adds no waits of its own before LDS reads of other buffers (its
+// tracking of DMA targets falls back to waiting for every DMA in flight);
+// callers await completion explicitly (vmcnt, then a barrier).  M0, the LDS
+// base of the instruction, is saved and restored around it.  The resource is
+// four SGPRs: base, base >> 32 (stride 0), size in bytes (reads past it return
+// zero without touching memory), 0x00020000 (32-bit untyped data).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)p),
+                 (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32)) & 0xffffu,
+                 (uint32_t)__builtin_amdgcn_readfirstlane(bytes), 0x00020000u};
+}
+__device__ __forceinline__ void dma16(u32x4 r, uint32_t lds, uint32_t voff) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(r)
+        : "memory");
+}
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)reinterpret_cast<uintptr_t>(
+        (__attribute__((address_space(3))) const char*)(
+            __attribute__((address_space(3))) const void*)p);
+}
+
 // Cross-lane exchange inside a wave64 (ds_bpermute based).
 __device__ __forceinline__ float xor_lane(float v, int mask) {
     return __shfl_xor(v, mask, kWave);

@@ -51,35 +51,6 @@ __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// One LDS-DMA instruction: each lane copies 16 bytes at voff from the buffer
-// `r` to LDS bytes [lds + 16 lane, lds + 16 lane + 16).  Issued as inline
-// assembly so that the compiler does not add waits of its own before LDS reads
-// of the other stages (its tracking of DMA targets falls back to waiting for
-// every DMA in flight); completion is awaited explicitly with vmcnt and a
-// barrier.  M0 (the LDS base of the DMA) is saved and restored around it.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
-    const uint64_t p = reinterpret_cast<uint64_t>(base);
-    return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)p),
-                 (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32)) & 0xffffu,
-                 (uint32_t)__builtin_amdgcn_readfirstlane(bytes), 0x00020000u};
-}
-__device__ __forceinline__ void dma16(u32x4 r, uint32_t lds, uint32_t voff) {
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(lds), "v"(voff), "s"(r)
-        : "memory");
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)reinterpret_cast<uintptr_t>((LDS_AS const char*)(LDS_AS const void*)p);
-}
-
 // blockIdx -> (token tile, feature tile).  Workgroups are dispatched
 // round-robin over the 8 XCDs (bid % 8), each with its own L2.  When the tile
 // grid splits 2 x 4, XCD x owns token half x / 4 and feature quarter x % 4
