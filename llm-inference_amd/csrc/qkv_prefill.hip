@@ -87,8 +87,8 @@ __global__ __launch_bounds__(kThreads, 1) void qkv_gemm_mfma(QkvGemmArgs a) {
     constexpr int kWaitOne = 0x0F70 | (kDmaPerWave & 15) | ((kDmaPerWave >> 4) << 14);
     static_assert(kDmaPerWave < 64, "vmcnt range");
 
-    // three stages, each operand buffer a distinct object so the compiler can
-    // tell the DMA into one stage from the reads of another
+    // three stages; the DMA is issued by dma16 (inline assembly), so the only
+    // waits between stages are the explicit vmcnt + barrier of each step
     __shared__ __attribute__((aligned(16))) f16 sa0[BM * kRowH];
     __shared__ __attribute__((aligned(16))) f16 sa1[BM * kRowH];
     __shared__ __attribute__((aligned(16))) f16 sa2[BM * kRowH];
