@@ -2,7 +2,8 @@
 libattn_mi355x.so.  CPU part: every function the header declares is defined in
 the library with the reference's exact signature (checked through the
 demangled names), and the reference-layout headers (kv_cache.hpp,
-rope_cache.hpp, gpu_utils.hpp) compile as C++17.  GPU part: the C++ test
+rope_cache.hpp, gpu_utils.hpp) compile as C++23 (the engine's standard) and
+as C++17.  GPU part: the C++ test
 program tests/cpp/test_reference_api.cpp, built against the library, runs the
 reference-style checks (decode KAT, RoPE/KV append, decode vs prefill rows,
 graph-captured multi-layer decode with node patching)."""
@@ -76,7 +77,10 @@ def test_library_defines_every_reference_launcher(attn):
     assert not missing, missing
 
 
-def test_reference_headers_compile(tmp_path):
+@pytest.mark.parametrize("std", ["c++17", "c++23"])
+def test_reference_headers_compile(tmp_path, std):
+    """The engine (model_inference.hpp) is C++23; the headers also stay valid
+    C++17 for other callers."""
     src = tmp_path / "use_headers.cpp"
     src.write_text(
         '#include "kernels/kernels.hpp"\n#include "kv_cache.hpp"\n#include "rope_cache.hpp"\n'
@@ -84,7 +88,7 @@ def test_reference_headers_compile(tmp_path):
         "static_assert(KV_CHUNK == 12);\n"
         "size_t f() { KVCache c{Cfg{}}; return c.layer_stride() + c.kv_dim(); }\n"
         "std::vector<float> g() { return compute_inverse_frequencies(128, 5.0e6f); }\n")
-    r = subprocess.run([HIPCC, "-std=c++17", "-fsyntax-only", "-I", str(ROOT / "include"), str(src)],
+    r = subprocess.run([HIPCC, f"-std={std}", "-fsyntax-only", "-I", str(ROOT / "include"), str(src)],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
 
@@ -105,7 +109,7 @@ def test_node_updaters_exit_through_hip_check(tmp_path, call):
                    f"int main() {{ {call}; std::puts(\"returned\"); return 0; }}\n")
     exe = tmp_path / "updater_failure"
     lib_dir = ROOT / "llm-inference_amd" / "lib"
-    r = subprocess.run([HIPCC, "-std=c++17", "-I", str(ROOT / "include"), str(src), "-o", str(exe),
+    r = subprocess.run([HIPCC, "-std=c++23", "-I", str(ROOT / "include"), str(src), "-o", str(exe),
                         "-L", str(lib_dir), "-lattn_mi355x", f"-Wl,-rpath,{lib_dir}"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
