@@ -176,6 +176,7 @@ enum Option {
     kOptDecodeHeadsPerGroup = 3,  // 0 = automatic; 1, 2 or 4 KV heads per split workgroup
     kOptQkvGemmForceGeneric = 4,
     kOptQkvGemmTokensPerWave = 5, // 0 = automatic; 32, 64 or 128
+    kOptQkvGemmWide = 6,          // 0 = automatic; 1 = never; 2 = whenever the shape allows
     kOptCount = 8
 };
 long get_option(int which);

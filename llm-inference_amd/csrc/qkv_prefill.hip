@@ -26,6 +26,9 @@
 //  * Workgroups are dispatched round-robin over the 8 XCDs; the tile grid is
 //    split over them (2 x 4 when it divides: each XCD owns half the token
 //    tiles and a quarter of the feature tiles, whose W rows stay in its L2).
+//  * From 7168 tokens (N a multiple of 384, Y 16-byte aligned) a 256 x 384
+//    tile of 8 waves (qkv_gemm_wide, below) replaces it: a third of the X
+//    re-reads and 1.5x the MFMA work per staged byte; identical results.
 //  * Epilogue: fp32 -> fp16 (the GEMM's output rounding), then for the fused
 //    kernel the rope.hip.cpp:44-58 rotation on those fp16 values (fp32
 //    products each rounded, no contraction): Q rows written rotated, K rows
@@ -38,6 +41,9 @@ namespace attn {
 namespace {
 
 constexpr int kBK = 64;      // k-values per stage
+// automatic use of the wide tile: from 28 token tiles (224 of the 256 CUs
+// busy at N = 3072); below that the 256 x 128 tile keeps more CUs busy
+constexpr uint32_t kWideMinTokens = 7168;
 constexpr int kRowH = kBK;   // halves per LDS row (128 B, no padding)
 constexpr int kThreads = 256;
 
@@ -306,6 +312,201 @@ __global__ __launch_bounds__(kThreads, 1) void qkv_gemm_mfma(QkvGemmArgs a) {
     }
 }
 
+// Wide tile for long prompts: a workgroup computes 256 tokens x 384 features
+// (three heads when D = 128) with 8 waves as 2 (tokens) x 4 (features), each
+// wave 128 x 96 on v_mfma_f32_32x32x16_f16, so every X and W byte staged in
+// LDS feeds 1.5x (X) and 3x (W) the MFMA work of the 256 x 128 tile and the
+// X re-reads from L2 drop by two thirds.  32 k-values per stage (64-byte LDS
+// rows, chunk c of row r at position c ^ ((r >> 2) & 3): conflict-free operand
+// reads), three stages of 40 KiB.  Each output sums its 16-value k-chunks in
+// the same order as qkv_gemm_mfma, so the two kernels give identical bits.
+// The epilogue runs one head at a time through LDS with the qkv_gemm_mfma
+// store pattern.
+constexpr int kWBM = 256;
+constexpr int kWBN = 384;
+constexpr int kWBK = 32;
+constexpr int kWThreads = 512;
+constexpr int kWADma = kWBM * 4 / 64;                  // 1 KiB DMA instructions per X stage (16)
+constexpr int kWBDma = kWBN * 4 / 64;                  // ... per W stage (24)
+constexpr int kWDmaPerWave = (kWADma + kWBDma) / 8;    // 5
+constexpr uint32_t kWStageA = kWBM * kWBK * 2;         // bytes of X per stage
+constexpr uint32_t kWStage = kWStageA + kWBN * kWBK * 2;  // bytes per stage (40 KiB)
+
+template <bool FUSED>
+__global__ __launch_bounds__(kWThreads, 1) void qkv_gemm_wide(QkvGemmArgs a) {
+    // vmcnt value that leaves one stage of this wave's DMA outstanding
+    constexpr int kWaitOne = 0x0F70 | kWDmaPerWave;
+    __shared__ __attribute__((aligned(16))) f16 lds[3 * kWStage / 2];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const uint32_t n = (uint32_t)lane & 31u, hh = (uint32_t)lane >> 5;
+
+    uint32_t m_tile, n_tile;
+    map_tile(blockIdx.x, a.m_tiles, a.n_tiles, m_tile, n_tile);
+    m_tile = __builtin_amdgcn_readfirstlane(m_tile);
+    n_tile = __builtin_amdgcn_readfirstlane(n_tile);
+    const uint32_t m0 = m_tile * kWBM, n0 = n_tile * kWBN;
+    const uint32_t K = a.K;
+    const uint32_t row_bytes = K * 2u;
+    const uint32_t rows_x = a.M - m0;   // >= 1
+    const uint32_t rows_w = a.N - n0;   // = 384 (N is a multiple of 384)
+    const f16* xb = a.x + (uint64_t)m0 * K;
+    const f16* wb = a.w + (uint64_t)n0 * K;
+
+    // DMA instruction t < 2 of a wave fills X bytes [1024 i, 1024 i + 1024)
+    // with i = wave + 8 t, the others W bytes with i = wave + 8 (t - 2); lane L
+    // writes 16-byte position p = 64 i + L: row p / 4, slot p % 4, which holds
+    // chunk slot ^ ((row >> 2) & 3)
+    uint32_t voff[kWDmaPerWave];
+#pragma unroll
+    for (int t = 0; t < kWDmaPerWave; ++t) {
+        const uint32_t ip = (uint32_t)(wave + 8 * (t < 2 ? t : t - 2));
+        const uint32_t p = 64u * ip + (uint32_t)lane;
+        const uint32_t row = p >> 2, slot = p & 3u;
+        voff[t] = row * row_bytes + 16u * (slot ^ ((row >> 2) & 3u));
+    }
+    const uint32_t lds0 = lds_addr(lds);
+    auto stage = [&](uint32_t kt) {
+        const uint32_t k0b = kt * (uint32_t)kWBK * 2u;
+        const u32x4 rx = rsrc_words(reinterpret_cast<const char*>(xb) + k0b,
+                                    rows_x * row_bytes - k0b);
+        const u32x4 rw = rsrc_words(reinterpret_cast<const char*>(wb) + k0b,
+                                    rows_w * row_bytes - k0b);
+        const uint32_t base = lds0 + (kt % 3u) * kWStage + 1024u * (uint32_t)wave;
+#pragma unroll
+        for (int t = 0; t < kWDmaPerWave; ++t) {
+            if (t < 2)
+                dma16(rx, base + 8192u * t, voff[t]);
+            else
+                dma16(rw, base + kWStageA + 8192u * (t - 2), voff[t]);
+        }
+    };
+
+    f32x16 acc[4][3];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 3; ++nt) acc[mt][nt] = f32x16{};
+
+    // operand rows: X rows 128 wm + 32 mt + n, W rows 96 wn + 32 nt + n; both
+    // start at a multiple of 32 plus n, so the swizzle is (n >> 2) & 3
+    const uint32_t sw = (n >> 2) & 3u;
+    const uint32_t a_row0 = 128u * (uint32_t)wm + n;
+    const uint32_t b_row0 = 96u * (uint32_t)wn + n;
+
+    auto compute = [&](uint32_t kt) {
+        const f16* sa = lds + (kt % 3u) * (kWStage / 2u);
+        const f16* sb = sa + kWStageA / 2u;
+#pragma unroll
+        for (int ks = 0; ks < kWBK / 16; ++ks) {
+            const uint32_t pos = 8u * (((uint32_t)(2 * ks) + hh) ^ sw);
+            f16x8 af[4], bf[3];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) af[mt] = lds16(sa + (a_row0 + 32u * mt) * kWBK + pos);
+#pragma unroll
+            for (int nt = 0; nt < 3; ++nt) bf[nt] = lds16(sb + (b_row0 + 32u * nt) * kWBK + pos);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 3; ++nt) acc[mt][nt] = mfma32(af[mt], bf[nt], acc[mt][nt]);
+        }
+    };
+
+    // stage kt sits in buffer kt % 3 (the pipeline of qkv_gemm_mfma)
+    const uint32_t KT = K / kWBK;
+    if (KT > 0) stage(0);
+    if (KT > 1) stage(1);
+    for (uint32_t kt = 0; kt < KT; ++kt) {
+        asm volatile("" ::: "memory");
+        if (kt + 1 < KT)
+            __builtin_amdgcn_s_waitcnt(kWaitOne);
+        else
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + 2 < KT) stage(kt + 2);
+        compute(kt);
+    }
+
+    // ---- epilogue, one head (128 features) per round.  acc[mt][nt][r] is
+    // token m0 + 128 wm + 32 mt + 8 (r / 4) + 4 hh + r % 4, tile feature
+    // f = 96 wn + 32 nt + n; a 32-feature block never straddles two heads.
+    f16* lo = lds;             // [256][64]: features 0..63 of the round's head
+    f16* hi = lds + kWBM * 64; // [256][64]: features 64..127
+    const uint32_t N = a.N;
+    const uint32_t j8 = 8u * ((uint32_t)tid & 7u), rsub = (uint32_t)tid >> 3;
+    const uint32_t Hq = a.num_heads, Hkv = a.num_kv_heads;
+    const uint64_t kv_dim = (uint64_t)Hkv * 128u;
+#pragma unroll 1
+    for (uint32_t h = 0; h < 3; ++h) {
+        __syncthreads();  // the stages (h = 0) or the previous round's tile are free
+#pragma unroll
+        for (int nt = 0; nt < 3; ++nt) {
+            const uint32_t fb = 96u * (uint32_t)wn + 32u * (uint32_t)nt;  // block's first feature
+            if (fb / 128u != h) continue;
+            const uint32_t c = (fb & 127u) + n;
+            f16* dst = (c < 64u ? lo : hi) + (c & 63u);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t row = 128u * (uint32_t)wm + 32u * mt + 8u * (r >> 2) + 4u * hh +
+                                         (r & 3);
+                    dst[row * 64u] = (f16)acc[mt][nt][r];
+                }
+        }
+        __syncthreads();
+        const uint32_t hn0 = n0 + 128u * h;  // first feature of the round's head
+        if (!FUSED) {
+#pragma unroll
+            for (int p = 0; p < kWBM / 64; ++p) {
+                const uint32_t row = 64u * p + rsub, m = m0 + row;
+                if (m >= a.M) break;
+                f16* yr = a.y + (uint64_t)m * N + hn0;
+                st16(yr + j8, lds16(lo + row * 64u + j8));
+                st16(yr + 64u + j8, lds16(hi + row * 64u + j8));
+            }
+            continue;
+        }
+        // fused: the round's tile is head hn0 / 128 (D = 128)
+        const uint32_t head = hn0 / 128u;
+        const bool is_q = head < Hq;
+        const bool is_k = !is_q && head < Hq + Hkv;
+        const bool rot = a.apply != 0 && (is_q || is_k);
+        f16* cache = is_q ? nullptr
+                          : (is_k ? a.kc + (uint64_t)(head - Hq) * 128u
+                                  : a.vc + (uint64_t)(head - Hq - Hkv) * 128u);
+#pragma unroll
+        for (int p = 0; p < kWBM / 64; ++p) {
+            const uint32_t row = 64u * p + rsub, m = m0 + row;
+            if (m >= a.M) break;
+            const f16x8 x0 = lds16(lo + row * 64u + j8);
+            const f16x8 x1 = lds16(hi + row * 64u + j8);
+            f16x8 r0 = x0, r1 = x1;
+            const uint64_t pos = (uint64_t)a.start_pos + m;
+            if (rot) {
+                const f16x8 cs = ld16(a.cos_t + pos * 64u + j8);
+                const f16x8 sn = ld16(a.sin_t + pos * 64u + j8);
+                rope_rotate8(x0, x1, cs, sn, r0, r1);
+            }
+            f16* yr = a.y + (uint64_t)m * N + hn0;
+            if (is_q) {
+                st16(yr + j8, r0);
+                st16(yr + 64u + j8, r1);
+            } else {
+                st16(yr + j8, x0);
+                st16(yr + 64u + j8, x1);
+                f16* cr = cache + pos * kv_dim;
+                st16(cr + j8, r0);
+                st16(cr + 64u + j8, r1);
+            }
+        }
+    }
+}
+
 // Any shape and alignment: one thread per output element, fp32 accumulation.
 // Block b covers token b / n_tiles, features 256 (b % n_tiles) + 0..255.
 __global__ __launch_bounds__(256) void qkv_gemm_generic(QkvGemmArgs a) {
@@ -340,6 +541,31 @@ hipError_t launch_mfma(const QkvGemmArgs& a, bool fused, hipStream_t stream) {
     return hipGetLastError();
 }
 
+hipError_t launch_wide(const QkvGemmArgs& a, bool fused, hipStream_t stream) {
+    QkvGemmArgs b = a;
+    b.n_tiles = a.N / kWBN;
+    b.vec_out = 1u;
+    b.m_tiles = (a.M + kWBM - 1u) / kWBM;
+    const uint64_t blocks = (uint64_t)b.m_tiles * b.n_tiles;
+    if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
+    if (fused)
+        hipLaunchKernelGGL(qkv_gemm_wide<true>, dim3((uint32_t)blocks), dim3(kWThreads), 0, stream,
+                           b);
+    else
+        hipLaunchKernelGGL(qkv_gemm_wide<false>, dim3((uint32_t)blocks), dim3(kWThreads), 0, stream,
+                           b);
+    return hipGetLastError();
+}
+
+// The wide tile needs whole 384-feature tiles and 16-byte aligned output
+// rows; it pays off once there are enough token tiles to fill the CUs.
+bool use_wide(const QkvGemmArgs& a) {
+    const long forced = get_option(kOptQkvGemmWide);
+    if (forced == 1) return false;
+    if (a.N % kWBN != 0 || a.K % kWBK != 0 || !aligned16(a.y)) return false;
+    return forced == 2 || a.M >= kWideMinTokens;
+}
+
 }  // namespace
 
 bool qkv_gemm_mfma_ok(const QkvGemmArgs& a) {
@@ -366,6 +592,7 @@ hipError_t launch_qkv_gemm_kernel(const QkvGemmArgs& a, bool fused, hipStream_t 
         hipLaunchKernelGGL(qkv_gemm_generic, dim3((uint32_t)blocks), dim3(256), 0, stream, b);
         return hipGetLastError();
     }
+    if (use_wide(a)) return launch_wide(a, fused, stream);
     switch (qkv_gemm_wmt(a.M)) {
         case 1: return launch_mfma<1>(a, fused, stream);
         case 2: return launch_mfma<2>(a, fused, stream);

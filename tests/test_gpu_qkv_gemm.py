@@ -220,3 +220,38 @@ def test_qkv_fused_prefill_pipeline_matches_reference_order(attn, gpu):
         torch.cuda.synchronize()
         outs.append(host(out))
     assert np.array_equal(outs[0], outs[1])
+
+
+def with_wide(attn, mode, fn):
+    attn.set_option("qkv_gemm_wide", mode)
+    try:
+        return fn()
+    finally:
+        attn.set_option("qkv_gemm_wide", 0)
+
+
+@pytest.mark.parametrize("M,N,K", [(700, TOTAL, HIDDEN), (256, 384, 64), (1, 384, 128),
+                                   (300, 1152, 512), (4100, TOTAL, HIDDEN)])
+def test_qkv_gemm_wide_tile_identical(attn, gpu, M, N, K):
+    """The 256 x 384 tile sums every output's k-chunks in the same order as
+    the 256 x 128 tile: identical bits, and the oracle bounds both."""
+    print(f"[case] gemm wide M={M} N={N} K={K}", flush=True)
+    x, w = rand_inputs(M, N, K, 9 + M)
+    narrow = with_wide(attn, 1, lambda: run_gemm(attn, gpu, x, w))
+    wide = with_wide(attn, 2, lambda: run_gemm(attn, gpu, x, w))
+    assert np.array_equal(wide, narrow)
+    check_vs_oracle(wide, x, w, np.unique(np.r_[0, M - 1, np.arange(0, M, 13)]))
+
+
+@pytest.mark.parametrize("M,start_pos,rotate", [(1000, 37, True), (300, 5, False),
+                                                (8192, 0, True), (257, 32000, True)])
+def test_qkv_gemm_wide_fused_identical(attn, gpu, M, start_pos, rotate):
+    """The fused wide tile writes the bytes of the fused 256 x 128 tile (Y and
+    every cache element, sentinel rows untouched)."""
+    print(f"[case] fused gemm wide M={M} pos={start_pos} rotate={rotate}", flush=True)
+    narrow = with_wide(attn, 1, lambda: fused_case(attn, gpu, M, start_pos, rotate))
+    wide = with_wide(attn, 2, lambda: fused_case(attn, gpu, M, start_pos, rotate))
+    for a_, b_, what in zip(wide[:4], narrow[:4], ("fused y", "fused cache", "two-step y",
+                                                   "two-step cache")):
+        assert np.array_equal(a_, b_), what
+    assert np.array_equal(wide[0], wide[2]) and np.array_equal(wide[1], wide[3])
