@@ -245,10 +245,12 @@ def bench_rope(torch, A, hipgraph, N, nbuf, steps, warmup, rotate=True, seed=6):
 def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769, producer="rope"):
     """36-layer attention-only decode step: per layer RoPE(+append) of one new
     token at position L-1 (NoPE on every 4th layer, model_inference.hpp:358)
-    and Flash-Decode over L keys, captured as one 72-node graph.  producer
-    "qkv_fused" / "qkv_two" start each layer from a hidden vector instead:
-    the QKV GEMV (2048 -> 3072, per-layer weights) fused with the RoPE/append
-    (72 nodes) or as the reference's two launches (108 nodes)."""
+    and Flash-Decode (split + merge) over L keys, captured as one 108-node
+    graph.  producer "rope_fused" issues each layer's RoPE/append and decode
+    as the decode's two kernels (attn_rope_store_kv_decode, 72 nodes).
+    producer "qkv_fused" / "qkv_two" start each layer from a hidden vector
+    instead: the QKV GEMV (2048 -> 3072, per-layer weights) fused with the
+    RoPE/append (108 nodes) or as the reference's two launches (144 nodes)."""
     dev = torch.device("cuda:0")
     S = L
     cache = torch.empty(layers * 2 * S * KV_DIM, dtype=torch.float16, device=dev)
@@ -268,7 +270,7 @@ def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769, producer="rope"):
     sp = stream.cuda_stream
     start_pos = L - 1
 
-    if producer != "rope":
+    if producer.startswith("qkv"):
         ws = rand16(torch, layers * QKV * HIDDEN, 600, 1.0 / 45)
         x = rand16(torch, HIDDEN, 599)
 
@@ -278,6 +280,13 @@ def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769, producer="rope"):
             kc = cb + 2 * (l * 2 * S * KV_DIM)
             vc = kc + 2 * S * KV_DIM
             apply = 1 if (l + 1) % 4 != 0 else 0
+            if producer == "rope_fused":
+                rc = lib.attn_rope_store_kv_decode(
+                    s, s + 2 * Q_DIM, s + 2 * (Q_DIM + KV_DIM), kc, vc, dcos.data_ptr(),
+                    dsin.data_ptr(), out[l].data_ptr(), po.data_ptr(), pm.data_ptr(),
+                    ps.data_ptr(), L, start_pos, HQ, HKV, D, 0, apply, sp, None, None)
+                assert rc == 0
+                continue
             if producer == "qkv_fused":
                 rc = lib.attn_qkv_rope_store_kv_decode(
                     x.data_ptr(), s, ws.data_ptr() + 2 * l * QKV * HIDDEN, kc, vc,
@@ -314,7 +323,7 @@ def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769, producer="rope"):
     ms = e0.elapsed_time(e1) / replays
     nrot = sum(1 for l in range(layers) if (l + 1) % 4 != 0)
     byts = layers * decode_bytes(L) + nrot * rope_bytes(1, True) + (layers - nrot) * rope_bytes(1, False)
-    if producer != "rope":
+    if producer.startswith("qkv"):
         byts += layers * qkv_bytes()
         del ws
     del cache
@@ -593,6 +602,12 @@ def main():
                                       "GBps": c5b / c5ms / 1e6,
                                       "pct_of_hbm_peak": 100 * c5b / c5ms / 1e6 / PEAK_HBM_GBS}
         log(f"C5 36-layer decode step: {c5ms * 1e3:.1f} us ({c5b / c5ms / 1e6:.0f} GB/s)")
+        c5fms, c5fb = bench_c5(torch, A, hipgraph, 10, producer="rope_fused")
+        detail["c5_36_layer_step_fused_rope_decode"] = {
+            "us": c5fms * 1e3, "bytes": c5fb, "GBps": c5fb / c5fms / 1e6,
+            "pct_of_hbm_peak": 100 * c5fb / c5fms / 1e6 / PEAK_HBM_GBS}
+        log(f"C5 with RoPE/append fused into the decode kernels: {c5fms * 1e3:.1f} us "
+            f"({c5fb / c5fms / 1e6:.0f} GB/s)")
         c5q = {p: bench_c5(torch, A, hipgraph, 10, producer=p) for p in ("qkv_fused", "qkv_two")}
         detail["c5_with_qkv_projection"] = {
             p: {"us": v[0] * 1e3, "bytes": v[1], "GBps": v[1] / v[0] / 1e6} for p, v in c5q.items()}

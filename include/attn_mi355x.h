@@ -99,6 +99,36 @@ int attn_update_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size
  * causal_attention.hip.cpp:1003-1026). */
 int attn_update_merge_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len);
 
+/* No single counterpart in the reference: launch_rope_and_store_kv(q, k, v,
+ * k_cache, v_cache, cos, sin, 1, Hq, Hkv, D, 0, 0, start_pos,
+ * apply_rotation) followed by launch_causal_attention_decode(q, k_cache,
+ * v_cache, out, partials, 1, kv_len, start_pos, Hq, Hkv, D, 0, kv_stride,
+ * stream, ...) -- the pair ModelInference issues per layer in every decode
+ * step (model_inference.hpp:96-126) -- as the decode's two kernels: the split
+ * kernel rotates q in registers and appends the new K (rotated) / V row
+ * before reading it, the merge kernel leaves q rotated in place.  q, the
+ * cache and out equal that pair's bit for bit.  Serves the MFMA decode path
+ * (head_dim 128, 16-byte aligned tensors) with kv_stride = Hkv*D (or 0) and
+ * start_pos < kv_len; other arguments return hipErrorInvalidValue and enqueue
+ * nothing (use the two launches).  The node handles are the split and merge
+ * kernels, patched together by attn_update_rope_decode_nodes. */
+int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16_t* v,
+                              attn_f16_t* k_cache, attn_f16_t* v_cache,
+                              const attn_f16_t* cos_table, const attn_f16_t* sin_table,
+                              attn_f16_t* out, float* partial_out, float* partial_max,
+                              float* partial_sum, size_t kv_len, size_t start_pos,
+                              size_t num_heads, size_t num_kv_heads, size_t head_dim,
+                              size_t kv_stride, int apply_rotation, hipStream_t stream,
+                              hipGraphNode_t* attention_node, hipGraphNode_t* merge_node);
+
+/* Patches both captured nodes of attn_rope_store_kv_decode to a new kv_len,
+ * start_pos and apply_rotation (what update_rope_and_store_kv_node,
+ * update_causal_attention_decode_node and update_merge_attention_decode_node
+ * do for the separate launches). */
+int attn_update_rope_decode_nodes(hipGraphExec_t graph_exec, hipGraphNode_t attention_node,
+                                  hipGraphNode_t merge_node, size_t kv_len, size_t start_pos,
+                                  int apply_rotation);
+
 /* Workspace states a caller must provide for kv_len keys:
  * num_heads * ceil(kv_len / ATTN_KV_CHUNK) (model_inference.hpp:192-198). */
 size_t attn_decode_workspace_states(size_t num_heads, size_t kv_len);

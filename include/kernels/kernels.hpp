@@ -180,6 +180,48 @@ void update_qkv_rope_and_store_kv_node(
     bool apply_rotation
 );
 
+// Not in the reference: launch_rope_and_store_kv for the decode token
+// followed by launch_causal_attention_decode (model_inference.hpp:96-126) as
+// the decode's two kernels (split, merge) with identical results: q is left
+// rotated in place, the new K/V row appended at start_pos, d_out holds the
+// attention.  head_dim 128, 16-byte aligned tensors, cache rows
+// num_kv_heads * head_dim apart and start_pos < kv_cache_len; other arguments
+// are reported like a failed launch and nothing is enqueued.
+void launch_rope_and_store_kv_decode(
+    __half* d_q,
+    const __half* d_k,
+    const __half* d_v,
+    __half* d_k_cache,
+    __half* d_v_cache,
+    const __half* d_cos,
+    const __half* d_sin,
+    __half* d_out,
+    float* d_partial_out,
+    float* d_partial_max,
+    float* d_partial_weight_sum,
+    size_t kv_cache_len,
+    size_t start_pos,
+    size_t num_heads,
+    size_t num_kv_heads,
+    size_t head_dim,
+    bool apply_rotation,
+    hipStream_t stream = nullptr,
+    hipGraphNode_t* attention_node = nullptr,
+    hipGraphNode_t* merge_node = nullptr
+);
+
+// Not in the reference: patches both captured nodes of
+// launch_rope_and_store_kv_decode (cf. update_rope_and_store_kv_node and the
+// two decode node updaters).
+void update_rope_and_store_kv_decode_nodes(
+    hipGraphExec_t graph_exec,
+    hipGraphNode_t attention_node,
+    hipGraphNode_t merge_node,
+    size_t kv_cache_len,
+    size_t start_pos,
+    bool apply_rotation
+);
+
 // Not in the reference: launch_qkv_gemm followed by launch_rope_and_store_kv
 // for a prefill of seq_len tokens (model_inference.hpp:266-285), fused into
 // one kernel (head_dim 128) with identical results.

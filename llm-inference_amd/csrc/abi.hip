@@ -448,6 +448,114 @@ int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t
     return 0;
 }
 
+int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16_t* v,
+                              attn_f16_t* k_cache, attn_f16_t* v_cache,
+                              const attn_f16_t* cos_table, const attn_f16_t* sin_table,
+                              attn_f16_t* out, float* partial_out, float* partial_max,
+                              float* partial_sum, size_t kv_len, size_t start_pos,
+                              size_t num_heads, size_t num_kv_heads, size_t head_dim,
+                              size_t kv_stride, int apply_rotation, hipStream_t stream,
+                              hipGraphNode_t* attention_node, hipGraphNode_t* merge_node) {
+    // the no-op shapes of both replaced launches (rope.hip.cpp:156,
+    // causal_attention.hip.cpp:860-866, :945-946)
+    if (kv_len == 0 || num_kv_heads == 0 || head_dim == 0) return 0;
+    if (num_heads % num_kv_heads != 0) return 0;
+    if (!fits_u32(kv_len) || !fits_u32(num_heads) || !fits_u32(head_dim))
+        return (int)hipErrorInvalidValue;
+    if (!q || !k || !v || !k_cache || !v_cache || !out || !partial_out || !partial_max ||
+        !partial_sum)
+        return (int)hipErrorInvalidValue;
+    if (apply_rotation && (!cos_table || !sin_table)) return (int)hipErrorInvalidValue;
+    const size_t kv_dim = num_kv_heads * head_dim;
+    const size_t kvs = kv_stride ? kv_stride : kv_dim;
+    // the fused kernels serve the MFMA decode path with the engine's cache
+    // layout (RoPE writes rows kv_dim apart, rope.hip.cpp:110) and the new
+    // token inside the decoded range; other calls use the two launches
+    if (kvs != kv_dim || start_pos >= kv_len) return (int)hipErrorInvalidValue;
+    const bool al = ((uintptr_t)k | (uintptr_t)v | (uintptr_t)cos_table | (uintptr_t)sin_table |
+                     (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return (int)e;
+    const DecodePlan p = plan_decode((uint32_t)kv_len, (uint32_t)num_heads,
+                                     (uint32_t)num_kv_heads, (uint32_t)head_dim, kvs, q,
+                                     k_cache, v_cache, device);
+    if (p.path == 0 || !al) return (int)hipErrorInvalidValue;
+    DecodeArgs a{};
+    a.q = reinterpret_cast<const f16*>(q);
+    a.k = reinterpret_cast<const f16*>(k_cache);
+    a.v = reinterpret_cast<const f16*>(v_cache);
+    a.out = reinterpret_cast<f16*>(out);
+    a.part_out = partial_out;
+    a.part_max = partial_max;
+    a.part_sum = partial_sum;
+    a.kv_stride = kvs;
+    a.kv_len = (uint32_t)kv_len;
+    a.num_heads = (uint32_t)num_heads;
+    a.num_kv_heads = (uint32_t)num_kv_heads;
+    a.group = (uint32_t)(num_heads / num_kv_heads);
+    a.head_dim = (uint32_t)head_dim;
+    a.scale_log2 = scale_log2_for(head_dim);
+    a.nsplit = p.nsplit;
+    a.chunk = p.chunk;
+    a.nstate = p.nstate;
+    a.q_rot = reinterpret_cast<f16*>(q);
+    a.k_dst = reinterpret_cast<f16*>(k_cache);
+    a.v_dst = reinterpret_cast<f16*>(v_cache);
+    a.k_src = reinterpret_cast<const f16*>(k);
+    a.v_src = reinterpret_cast<const f16*>(v);
+    a.cos_t = reinterpret_cast<const f16*>(cos_table);
+    a.sin_t = reinterpret_cast<const f16*>(sin_table);
+    a.row = (uint32_t)start_pos;
+    a.apply = apply_rotation ? 1u : 0u;
+    e = launch_decode_split(a, p, stream, true);
+    if (e != hipSuccess) return (int)e;
+    if (attention_node) {
+        e = captured_node(stream, attention_node);
+        if (e != hipSuccess) return (int)e;
+    }
+    e = launch_decode_merge(a, stream, true);
+    if (e != hipSuccess) return (int)e;
+    if (merge_node) {
+        e = captured_node(stream, merge_node);
+        if (e != hipSuccess) return (int)e;
+    }
+    return 0;
+}
+
+int attn_update_rope_decode_nodes(hipGraphExec_t graph_exec, hipGraphNode_t attention_node,
+                                  hipGraphNode_t merge_node, size_t kv_len, size_t start_pos,
+                                  int apply_rotation) {
+    if (kv_len == 0 || !fits_u32(kv_len) || start_pos >= kv_len) return (int)hipErrorInvalidValue;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return (int)e;
+    for (int m = 0; m < 2; ++m) {
+        hipGraphNode_t node = m ? merge_node : attention_node;
+        hipKernelNodeParams params{};
+        e = hipGraphKernelNodeGetParams(node, &params);
+        if (e != hipSuccess) return (int)e;
+        const bool ok = m ? params.func == decode_merge_symbol(true)
+                          : (params.func == decode_split_symbol(1, true) ||
+                             params.func == decode_split_symbol(2, true) ||
+                             params.func == decode_split_symbol(3, true));
+        if (!ok) return (int)hipErrorInvalidValue;
+        DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(params.kernelParams[0]);
+        a.kv_len = (uint32_t)kv_len;
+        a.row = (uint32_t)start_pos;
+        a.apply = apply_rotation ? 1u : 0u;
+        if (a.apply && (!a.cos_t || !a.sin_t)) return (int)hipErrorInvalidValue;
+        replan_decode(a, device);
+        void* args[1] = {&a};
+        params.kernelParams = args;
+        params.extra = nullptr;
+        if (!m) params.gridDim.x = a.nsplit;
+        e = hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
+        if (e != hipSuccess) return (int)e;
+    }
+    return 0;
+}
+
 static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len,
                              bool merge) {
     if (kv_len == 0 || !fits_u32(kv_len)) return (int)hipErrorInvalidValue;

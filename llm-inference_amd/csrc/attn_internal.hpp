@@ -104,6 +104,19 @@ struct DecodeArgs {
     uint32_t chunk;      // keys per split (patched)
     uint32_t nstate;     // partial states per query head (patched)
     float scale_log2;    // log2(e) / sqrt(D)
+    // fused RoPE + KV append of the decoded token (the ROPE kernel variants):
+    // q rotated in registers by the split kernel and in place by the merge
+    // kernel; cache row `row` of K (rotated) and V written from k_src / v_src
+    // by the split workgroups whose chunk holds it, before they read it
+    f16* q_rot;          // = q, writable
+    f16* k_dst;          // = k, writable (cache rows kv_stride apart)
+    f16* v_dst;
+    const f16* k_src;    // [Hkv][D] of the new token
+    const f16* v_src;
+    const f16* cos_t;    // [S][D/2]
+    const f16* sin_t;
+    uint32_t row;        // cache row of the new token (start_pos, patched)
+    uint32_t apply;      // 1: rotate q and K; 0: copy K and V only (patched)
 };
 
 struct DecodePlan {
@@ -121,10 +134,11 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
 // Used by launch and by the graph-node updaters (same plan for the same L).
 void replan_decode(DecodeArgs& a, int device);
 // Enqueues the split kernel and the merge kernel (two graph nodes).
-hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream);
-hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
-const void* decode_split_symbol(int path);
-const void* decode_merge_symbol();
+hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,
+                               bool rope = false);
+hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream, bool rope = false);
+const void* decode_split_symbol(int path, bool rope = false);
+const void* decode_merge_symbol(bool rope = false);
 
 // ------------------------------------------------------------- prefill
 struct PrefillArgs {

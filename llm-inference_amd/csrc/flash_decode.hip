@@ -61,7 +61,7 @@ struct KVBatch {
 // waves of a workgroup read whole cache rows (all KV heads of a token)
 // together.  With one 8-wave workgroup per CU and two batches per wave, every
 // load of the kernel is issued at its start.
-template <int HPW>
+template <int HPW, bool ROPE>
 __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     constexpr int WAVES = 8;
     constexpr int kThreads = WAVES * 64;
@@ -95,9 +95,48 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
         const f16* qp = a.q + (uint64_t)(g * G + n) * kD + 8 * gq;
 #pragma unroll
         for (int s = 0; s < 4; ++s) qb[s] = ld16(qp + 32 * s);
+        if constexpr (ROPE) {
+            // dims 32s + 8gq + i (s = 0, 1) pair with 64 more (s + 2): the lane
+            // holds both halves of 16 rotation pairs (rope.hip.cpp:44-58)
+            if (a.apply) {
+                const f16* ct = a.cos_t + (uint64_t)a.row * (kD / 2) + 8 * gq;
+                const f16* st = a.sin_t + (uint64_t)a.row * (kD / 2) + 8 * gq;
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    rope_rotate8(qb[s], qb[s + 2], ld16(ct + 32 * s), ld16(st + 32 * s), qb[s],
+                                 qb[s + 2]);
+            }
+        }
     } else {
 #pragma unroll
         for (int s = 0; s < 4; ++s) qb[s] = f16x8{};
+    }
+    if constexpr (ROPE) {
+        // the workgroups whose chunk holds the new token's row append it
+        // (K rotated, V copied) and only then read the chunk: the stores are
+        // complete (vmcnt) and the barrier orders them before every wave's
+        // loads; no other workgroup reads that row's bytes of these heads
+        if (a.row >= t0 && a.row - t0 < nk) {
+            if (phase == 0 && lane < 16) {
+                const uint64_t src = (uint64_t)g * kD;
+                const uint64_t dst = (uint64_t)a.row * a.kv_stride + (uint64_t)g * kD;
+                if (lane < 8) {  // K: dims 8 lane .. +7 and their partners 64 + 8 lane ..
+                    const uint32_t c8 = 8u * (uint32_t)lane;
+                    f16x8 k0 = ld16(a.k_src + src + c8), k1 = ld16(a.k_src + src + 64 + c8);
+                    if (a.apply)
+                        rope_rotate8(k0, k1, ld16(a.cos_t + (uint64_t)a.row * (kD / 2) + c8),
+                                     ld16(a.sin_t + (uint64_t)a.row * (kD / 2) + c8), k0, k1);
+                    st16(a.k_dst + dst + c8, k0);
+                    st16(a.k_dst + dst + 64 + c8, k1);
+                } else {         // V: 16 bytes per lane
+                    const uint32_t c16 = 16u * (uint32_t)(lane - 8);
+                    st16(a.v_dst + dst + c16, ld16(a.v_src + src + c16));
+                    st16(a.v_dst + dst + c16 + 8, ld16(a.v_src + src + c16 + 8));
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the row is written
+            __syncthreads();
+        }
     }
 
     // S^T row m of tile tt is key 8*(m/4) + 4*tt + (m%4) of the batch, so the
@@ -240,6 +279,7 @@ __device__ __forceinline__ f32x4 buf_ldf4(BufRsrc r, uint32_t byte_off) {
 // (all loads of a round issued first, through range-checked buffer
 // resources: splits past nstate read as zero and get weight 0); the 64 lanes
 // then combine with xor shuffles -- no LDS, no barrier.
+template <bool ROPE>
 __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
     const uint32_t lane = threadIdx.x;
     const uint32_t h = blockIdx.x;
@@ -299,6 +339,19 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
         for (int e = 1; e < 4; ++e) v = lane == (uint32_t)e ? num[e] : v;
         a.out[(uint64_t)h * kD + d0 + lane] = (f16)(v / den);
     }
+    if constexpr (ROPE) {
+        // q rotated in place, as launch_rope_and_store_kv leaves it; every
+        // split workgroup has read it (the kernel boundary orders this)
+        if (a.apply && blockIdx.y < 8 && lane == 0) {
+            const uint32_t c8 = 8u * blockIdx.y;
+            f16* qh = a.q_rot + (uint64_t)h * kD;
+            f16x8 x0 = ld16(qh + c8), x1 = ld16(qh + 64 + c8);
+            rope_rotate8(x0, x1, ld16(a.cos_t + (uint64_t)a.row * (kD / 2) + c8),
+                         ld16(a.sin_t + (uint64_t)a.row * (kD / 2) + c8), x0, x1);
+            st16(qh + c8, x0);
+            st16(qh + 64 + c8, x1);
+        }
+    }
 }
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -306,14 +359,23 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 }  // namespace
 
 // path 1/2/3: 4/2/1 KV heads per workgroup
-const void* decode_split_symbol(int path) {
-    if (path == 1) return reinterpret_cast<const void*>(&flash_decode_split<4>);
-    if (path == 2) return reinterpret_cast<const void*>(&flash_decode_split<2>);
-    if (path == 3) return reinterpret_cast<const void*>(&flash_decode_split<1>);
+const void* decode_split_symbol(int path, bool rope) {
+    if (rope) {
+        if (path == 1) return reinterpret_cast<const void*>(&flash_decode_split<4, true>);
+        if (path == 2) return reinterpret_cast<const void*>(&flash_decode_split<2, true>);
+        if (path == 3) return reinterpret_cast<const void*>(&flash_decode_split<1, true>);
+        return nullptr;
+    }
+    if (path == 1) return reinterpret_cast<const void*>(&flash_decode_split<4, false>);
+    if (path == 2) return reinterpret_cast<const void*>(&flash_decode_split<2, false>);
+    if (path == 3) return reinterpret_cast<const void*>(&flash_decode_split<1, false>);
     return generic_attention_symbol();
 }
 
-const void* decode_merge_symbol() { return reinterpret_cast<const void*>(&flash_decode_merge); }
+const void* decode_merge_symbol(bool rope) {
+    return rope ? reinterpret_cast<const void*>(&flash_decode_merge<true>)
+                : reinterpret_cast<const void*>(&flash_decode_merge<false>);
+}
 
 DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_heads,
                        uint32_t head_dim, uint64_t kv_stride, const void* q, const void* k,
@@ -361,25 +423,20 @@ void replan_decode(DecodeArgs& a, int device) {
     a.nstate = p.nstate;
 }
 
-hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
+hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,
+                               bool rope) {
     const int hpw = p.path == 1 ? 4 : p.path == 2 ? 2 : 1;
     const dim3 grid(a.nsplit, a.num_kv_heads / hpw);
-    if (p.path == 1) {
-        hipLaunchKernelGGL(flash_decode_split<4>, grid, dim3(512), 0, stream, a);
-    } else if (p.path == 2) {
-        hipLaunchKernelGGL(flash_decode_split<2>, grid, dim3(512), 0, stream, a);
-    } else if (p.path == 3) {
-        hipLaunchKernelGGL(flash_decode_split<1>, grid, dim3(512), 0, stream, a);
-    } else {
-        return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    if (p.path < 1 || p.path > 3) return hipErrorInvalidValue;
+    const void* fn = decode_split_symbol(p.path, rope);
+    void* args[1] = {const_cast<DecodeArgs*>(&a)};
+    return hipLaunchKernel(fn, grid, dim3(512), args, 0, stream);
 }
 
-hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(flash_decode_merge, dim3(a.num_heads, kD / kMergeDims), dim3(64), 0,
-                       stream, a);
-    return hipGetLastError();
+hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream, bool rope) {
+    void* args[1] = {const_cast<DecodeArgs*>(&a)};
+    return hipLaunchKernel(decode_merge_symbol(rope), dim3(a.num_heads, kD / kMergeDims),
+                           dim3(64), args, 0, stream);
 }
 
 }  // namespace attn

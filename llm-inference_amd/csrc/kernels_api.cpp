@@ -134,6 +134,33 @@ void launch_causal_attention_decode_vectorized(
                                    kv_stride, stream, attention_node, merge_node);
 }
 
+void launch_rope_and_store_kv_decode(__half* d_q, const __half* d_k, const __half* d_v,
+                                     __half* d_k_cache, __half* d_v_cache, const __half* d_cos,
+                                     const __half* d_sin, __half* d_out, float* d_partial_out,
+                                     float* d_partial_max, float* d_partial_weight_sum,
+                                     size_t kv_cache_len, size_t start_pos, size_t num_heads,
+                                     size_t num_kv_heads, size_t head_dim, bool apply_rotation,
+                                     hipStream_t stream, hipGraphNode_t* attention_node,
+                                     hipGraphNode_t* merge_node) {
+    const int rc = attn_rope_store_kv_decode(
+        h(d_q), h(d_k), h(d_v), h(d_k_cache), h(d_v_cache), h(d_cos), h(d_sin), h(d_out),
+        d_partial_out, d_partial_max, d_partial_weight_sum, kv_cache_len, start_pos, num_heads,
+        num_kv_heads, head_dim, 0, apply_rotation ? 1 : 0, stream, attention_node, merge_node);
+    // gpu_utils.hpp:45-59: a capture that does not end in exactly one node throws
+    if (rc == (int)hipErrorIllegalState && (attention_node || merge_node))
+        throw std::runtime_error("Expected one capture dependency");
+    report(rc);
+}
+
+void update_rope_and_store_kv_decode_nodes(hipGraphExec_t graph_exec,
+                                           hipGraphNode_t attention_node,
+                                           hipGraphNode_t merge_node, size_t kv_cache_len,
+                                           size_t start_pos, bool apply_rotation) {
+    HIP_CHECK((hipError_t)attn_update_rope_decode_nodes(graph_exec, attention_node, merge_node,
+                                                        kv_cache_len, start_pos,
+                                                        apply_rotation ? 1 : 0));
+}
+
 void update_merge_attention_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node,
                                         size_t kv_cache_len) {
     HIP_CHECK((hipError_t)attn_update_merge_node(graph_exec, node, kv_cache_len));

@@ -59,6 +59,9 @@ def _declare(lib):
         "attn_update_qkv_rope_node": (_c.c_int, [_vp, _vp, _sz, _c.c_int]),
         "attn_qkv_gemm": (_c.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
         "attn_qkv_gemm_rope_store_kv": (_c.c_int, [_vp] * 7 + [_sz] * 6 + [_c.c_int, _vp]),
+        "attn_rope_store_kv_decode": (_c.c_int, [_vp] * 11 + [_sz] * 6 + [_c.c_int, _vp, _vp,
+                                                                          _vp]),
+        "attn_update_rope_decode_nodes": (_c.c_int, [_vp, _vp, _vp, _sz, _sz, _c.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -84,7 +87,8 @@ def exported_symbols():
             "attn_decode_workspace_states", "attn_rope_tables", "attn_decode_plan",
             "attn_prefill_plan", "attn_set_option", "attn_version", "attn_qkv_decode",
             "attn_qkv_rope_store_kv_decode", "attn_update_qkv_rope_node", "attn_qkv_gemm",
-            "attn_qkv_gemm_rope_store_kv"]
+            "attn_qkv_gemm_rope_store_kv", "attn_rope_store_kv_decode",
+            "attn_update_rope_decode_nodes"]
 
 
 def _ptr(x) -> Optional[int]:
@@ -198,6 +202,31 @@ def decode(q, k_cache, v_cache, out, partial_out, partial_max, partial_sum, quer
                            kv_len, start_pos, num_heads, num_kv_heads, head_dim, q_stride,
                            kv_stride, _stream(stream), None, None)
     _check(rc, "attn_decode")
+
+
+def rope_store_kv_decode(q, k, v, k_cache, v_cache, cos, sin, out, partial_out, partial_max,
+                         partial_sum, kv_len, start_pos, num_heads, num_kv_heads, head_dim,
+                         apply_rotation=True, kv_stride=0, stream=None, nodes=None):
+    """launch_rope_and_store_kv + launch_causal_attention_decode for one decode
+    token as the decode's two kernels (no reference counterpart).  `nodes`, a
+    list, receives the (split, merge) graph nodes when capturing."""
+    an, mn = ctypes.c_void_p(), ctypes.c_void_p()
+    rc = lib().attn_rope_store_kv_decode(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache), _ptr(cos), _ptr(sin), _ptr(out),
+        _ptr(partial_out), _ptr(partial_max), _ptr(partial_sum), kv_len, start_pos, num_heads,
+        num_kv_heads, head_dim, kv_stride, 1 if apply_rotation else 0, _stream(stream),
+        ctypes.byref(an) if nodes is not None else None,
+        ctypes.byref(mn) if nodes is not None else None)
+    _check(rc, "attn_rope_store_kv_decode")
+    if nodes is not None:
+        nodes[:] = [an.value, mn.value]
+
+
+def update_rope_decode_nodes(graph_exec, attention_node, merge_node, kv_len, start_pos,
+                             apply_rotation=True):
+    rc = lib().attn_update_rope_decode_nodes(graph_exec, attention_node, merge_node, kv_len,
+                                             start_pos, 1 if apply_rotation else 0)
+    _check(rc, "attn_update_rope_decode_nodes")
 
 
 def decode_plan(kv_len, num_heads, num_kv_heads, head_dim, kv_stride=0, q=None, k=None,

@@ -15,7 +15,10 @@
 //   6. A graph-captured decode step built on the fused
 //      launch_qkv_rope_and_store_kv_decode (patched per token) against eager
 //      launch_qkv_decode + launch_rope_and_store_kv + decode, bit for bit.
-//   7. launch_qkv_gemm against an fp64 CPU product, and the fused
+//   7. A graph-captured decode step built on the fused
+//      launch_rope_and_store_kv_decode (both nodes patched per token) against
+//      eager launch_rope_and_store_kv + decode, bit for bit.
+//   8. launch_qkv_gemm against an fp64 CPU product, and the fused
 //      launch_qkv_gemm_rope_and_store_kv against the two launches, bit for bit.
 // Prints one PASS/FAIL line per test; exit status is the number of failures.
 #include <hip/hip_fp16.h>
@@ -576,6 +579,104 @@ void test_graph_fused_qkv_decode_step() {
 }
 
 // ---------------------------------------------------------------- test 7
+// launch_rope_and_store_kv_decode (not in the reference) captured per layer
+// and patched per step with update_rope_and_store_kv_decode_nodes: q, the
+// caches and the outputs equal the reference's launch_rope_and_store_kv +
+// launch_causal_attention_decode_vectorized bit for bit at every step.
+void test_graph_fused_rope_decode_step() {
+    const size_t layers = 4, heads = 16, kv_heads = 4, head_dim = 128;
+    const size_t q_dim = heads * head_dim, kv_dim = kv_heads * head_dim, total = q_dim + 2 * kv_dim;
+    const size_t prompt = 3000, steps = 4;
+    Config cfg{layers, prompt + steps + 1, kv_heads, head_dim};
+    KVCache graph_cache(cfg), eager_cache(cfg);
+    RopeCache rope = create_rope_cache(cfg.max_seq_len, head_dim, 5.0e6f);
+    std::mt19937 gen(12);
+    std::normal_distribution<float> nd;
+    std::vector<__half> cache_init(cfg.num_layers * 2 * cfg.max_seq_len * kv_dim);
+    for (auto& v : cache_init) v = __float2half(nd(gen));
+    HIP_CHECK(hipMemcpy(graph_cache.get_k_cache(0), cache_init.data(), cache_init.size() * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(eager_cache.get_k_cache(0), cache_init.data(), cache_init.size() * 2, hipMemcpyHostToDevice));
+    __half *y_g, *y_e, *out_g, *out_e;
+    HIP_CHECK(hipMalloc(&y_g, layers * total * 2));
+    HIP_CHECK(hipMalloc(&y_e, layers * total * 2));
+    HIP_CHECK(hipMalloc(&out_g, layers * q_dim * 2));
+    HIP_CHECK(hipMalloc(&out_e, layers * q_dim * 2));
+    const size_t cap = heads * ((cfg.max_seq_len + KV_CHUNK - 1) / KV_CHUNK);
+    float *po, *pm, *ps;
+    HIP_CHECK(hipMalloc(&po, cap * head_dim * 4));
+    HIP_CHECK(hipMalloc(&pm, cap * 4));
+    HIP_CHECK(hipMalloc(&ps, cap * 4));
+    hipStream_t stream;
+    HIP_CHECK(hipStreamCreate(&stream));
+    struct Nodes { hipGraphNode_t attention, merge; };
+    std::vector<Nodes> nodes(layers);
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    auto enqueue_fused = [&](size_t start_pos) {
+        for (size_t l = 0; l < layers; ++l) {
+            __half* a = y_g + l * total;
+            launch_rope_and_store_kv_decode(a, a + q_dim, a + q_dim + kv_dim,
+                                            graph_cache.get_k_cache(l), graph_cache.get_v_cache(l),
+                                            rope.d_cos, rope.d_sin, out_g + l * q_dim, po, pm, ps,
+                                            start_pos + 1, start_pos, heads, kv_heads, head_dim,
+                                            (l + 1) % 4 != 0, stream, &nodes[l].attention,
+                                            &nodes[l].merge);
+        }
+    };
+    auto enqueue_two = [&](size_t start_pos) {
+        for (size_t l = 0; l < layers; ++l) {
+            __half* a = y_e + l * total;
+            launch_rope_and_store_kv(a, a + q_dim, a + q_dim + kv_dim, eager_cache.get_k_cache(l),
+                                     eager_cache.get_v_cache(l), rope.d_cos, rope.d_sin, 1,
+                                     heads, kv_heads, head_dim, total, total, start_pos,
+                                     (l + 1) % 4 != 0, stream);
+            launch_causal_attention_decode_vectorized(
+                a, eager_cache.get_k_cache(l), eager_cache.get_v_cache(l), out_e + l * q_dim, po,
+                pm, ps, 1, start_pos + 1, start_pos, heads, kv_heads, head_dim, total, kv_dim,
+                stream, nullptr, nullptr);
+        }
+    };
+    bool all = true;
+    std::vector<__half> qkv(layers * total);
+    for (size_t step = 0; step < steps; ++step) {
+        const size_t start_pos = prompt + step;
+        for (auto& v : qkv) v = __float2half(nd(gen));
+        HIP_CHECK(hipMemcpy(y_g, qkv.data(), qkv.size() * 2, hipMemcpyHostToDevice));
+        HIP_CHECK(hipMemcpy(y_e, qkv.data(), qkv.size() * 2, hipMemcpyHostToDevice));
+        if (!exec) {
+            HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeGlobal));
+            enqueue_fused(start_pos);
+            HIP_CHECK(hipStreamEndCapture(stream, &graph));
+            HIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+        } else {
+            for (size_t l = 0; l < layers; ++l)
+                update_rope_and_store_kv_decode_nodes(exec, nodes[l].attention, nodes[l].merge,
+                                                      start_pos + 1, start_pos, (l + 1) % 4 != 0);
+        }
+        HIP_CHECK(hipGraphLaunch(exec, stream));
+        HIP_CHECK(hipStreamSynchronize(stream));
+        enqueue_two(start_pos);
+        HIP_CHECK(hipStreamSynchronize(stream));
+        const auto og = download(out_g, layers * q_dim), oe = download(out_e, layers * q_dim);
+        const auto yg = download(y_g, layers * total), ye = download(y_e, layers * total);
+        const auto cg = download(graph_cache.get_k_cache(0), cache_init.size());
+        const auto ce = download(eager_cache.get_k_cache(0), cache_init.size());
+        if (!(same_bits(og.data(), oe.data(), og.size()) && same_bits(yg.data(), ye.data(), yg.size()) &&
+              same_bits(cg.data(), ce.data(), cg.size()))) {
+            std::printf("  fused rope+decode graph / two-launch mismatch at step %zu\n", step);
+            all = false;
+        }
+    }
+    HIP_CHECK(hipGraphExecDestroy(exec));
+    HIP_CHECK(hipGraphDestroy(graph));
+    HIP_CHECK(hipStreamDestroy(stream));
+    for (void* p : {(void*)y_g, (void*)y_e, (void*)out_g, (void*)out_e, (void*)po, (void*)pm,
+                    (void*)ps})
+        HIP_CHECK(hipFree(p));
+    report("graph_fused_rope_decode_step", all);
+}
+
+// ---------------------------------------------------------------- test 8
 void test_qkv_gemm_prefill() {
     const size_t heads = 16, kv_heads = 4, head_dim = 128, hidden = 2048, tokens = 70;
     const size_t q_dim = heads * head_dim, kv_dim = kv_heads * head_dim, total = q_dim + 2 * kv_dim;
@@ -643,6 +744,7 @@ int main() {
     test_graph_decode_step();
     test_qkv_decode_reference_gemv();
     test_graph_fused_qkv_decode_step();
+    test_graph_fused_rope_decode_step();
     test_qkv_gemm_prefill();
     std::printf("%d failure(s)\n", g_failures);
     return g_failures;

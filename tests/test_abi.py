@@ -74,6 +74,10 @@ def test_noop_shapes_touch_nothing(attn):
     assert lib.attn_qkv_decode(None, None, None, 2048, 0, None) == 0
     assert lib.attn_qkv_rope_store_kv_decode(None, None, None, None, None, None, None, 2048, 0, 0,
                                              128, 0, 1, None) == 0
+    # fused RoPE + decode: the no-op shapes of both launches it replaces
+    for L, hq, hkv, d in ((0, 16, 4, 128), (5, 16, 0, 128), (5, 16, 4, 0), (5, 16, 3, 128)):
+        assert lib.attn_rope_store_kv_decode(*([None] * 11), L, 0, hq, hkv, d, 0, 1, None, None,
+                                             None) == 0
 
 
 def test_invalid_arguments_are_errors(attn):
@@ -101,6 +105,18 @@ def test_invalid_arguments_are_errors(attn):
     assert lib.attn_qkv_rope_store_kv_decode(16, y, 16, 16, 16, None, 16, 2048, 16, 4, 128, 0, 1,
                                              None) != 0
     assert lib.attn_update_qkv_rope_node(None, None, 0, 1) != 0
+    # fused RoPE + decode: null pointers, missing tables when rotating, cache
+    # rows not kv_dim apart, the new token outside the decoded range
+    p = [16] * 11
+    def fused(ptrs, L=64, pos=63, kvs=0, apply=1):
+        return lib.attn_rope_store_kv_decode(*ptrs, L, pos, 16, 4, 128, kvs, apply, None, None,
+                                             None)
+    assert fused([None] + p[1:]) != 0
+    assert fused(p[:5] + [None] + p[6:]) != 0
+    assert fused(p, kvs=520) != 0
+    assert fused(p, pos=64) != 0
+    assert lib.attn_update_rope_decode_nodes(None, None, None, 64, 64, 1) != 0
+    assert lib.attn_update_rope_decode_nodes(None, None, None, 0, 0, 1) != 0
 
 
 def test_decode_plan_respects_workspace_capacity(attn):

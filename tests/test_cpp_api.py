@@ -6,7 +6,8 @@ rope_cache.hpp, gpu_utils.hpp) compile as C++23 (the engine's standard) and
 as C++17.  GPU part: the C++ test
 program tests/cpp/test_reference_api.cpp, built against the library, runs the
 reference-style checks (decode KAT, RoPE/KV append, decode vs prefill rows,
-graph-captured multi-layer decode with node patching)."""
+graph-captured multi-layer decode with node patching, the fused QKV and
+RoPE + decode launchers against the reference's launch sequences)."""
 import pathlib
 import re
 import subprocess
@@ -50,6 +51,13 @@ EXPECTED = {
     "__half const*, __half const*, unsigned long, unsigned long, unsigned long, unsigned long, "
     "unsigned long, bool, ihipStream_t*)",
     "update_qkv_rope_and_store_kv_node(hipGraphExec*, hipGraphNode*, unsigned long, bool)",
+    # fused RoPE + decode (no reference counterpart)
+    "launch_rope_and_store_kv_decode(__half*, __half const*, __half const*, __half*, __half*, "
+    "__half const*, __half const*, __half*, float*, float*, float*, unsigned long, unsigned long, "
+    "unsigned long, unsigned long, unsigned long, bool, ihipStream_t*, hipGraphNode**, "
+    "hipGraphNode**)",
+    "update_rope_and_store_kv_decode_nodes(hipGraphExec*, hipGraphNode*, hipGraphNode*, "
+    "unsigned long, unsigned long, bool)",
 }
 
 
@@ -98,6 +106,7 @@ def test_reference_headers_compile(tmp_path, std):
     "update_causal_attention_decode_node(nullptr, nullptr, 5)",
     "update_merge_attention_decode_node(nullptr, nullptr, 5)",
     "update_qkv_rope_and_store_kv_node(nullptr, nullptr, 5, true)",
+    "update_rope_and_store_kv_decode_nodes(nullptr, nullptr, nullptr, 5, 4, true)",
 ])
 def test_node_updaters_exit_through_hip_check(tmp_path, call):
     """The reference's updaters wrap hipGraphExecKernelNodeSetParams in
@@ -126,5 +135,5 @@ def test_cpp_reference_api_program(gpu):
     print(r.stdout)
     print(r.stderr)
     lines = [l for l in r.stdout.splitlines() if l.startswith(("PASS", "FAIL"))]
-    assert len(lines) == 8, r.stdout + r.stderr
+    assert len(lines) == 9, r.stdout + r.stderr
     assert r.returncode == 0, r.stdout + r.stderr
