@@ -447,6 +447,14 @@ def profile_workload(torch, A):
                  KV_DIM)
     torch.cuda.synchronize()
     log(f"profile: 16 decode calls L={L} (algorithmic {decode_bytes(L)} B each)")
+    rcos, rsin = A.rope_tables(L, D, THETA)
+    rcos, rsin = rcos.to(dev), rsin.to(dev)
+    knew, vnew = rand16(torch, KV_DIM, 30), rand16(torch, KV_DIM, 31)
+    for i in range(16):
+        A.rope_store_kv_decode(q, knew, vnew, ks[i % nbuf], vs[i % nbuf], rcos, rsin, out, po, pm,
+                               ps, L, L - 1, HQ, HKV, D, True)
+    torch.cuda.synchronize()
+    log(f"profile: 16 fused RoPE + append + decode calls L={L}")
     del ks, vs
     N = 8192
     qkv = rand16(torch, N * QKV, 4, 0.5)
