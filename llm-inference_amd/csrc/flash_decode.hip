@@ -35,6 +35,11 @@
 //    l = sum_c 2^(m_c-M) l_c, out = sum_c 2^(m_c-M) acc_c / l (an online merge
 //    per lane over 16-byte partial loads, then xor shuffles).
 //    The kernel boundary orders the partial writes before the merge reads.
+//  * ROPE variants (attn_rope_store_kv_decode): the decode token's RoPE + KV
+//    append (rope.hip.cpp:61-134 for one token) folded into the two kernels:
+//    the split kernel rotates q in registers and the workgroups whose chunk
+//    holds the new row write it before reading their chunk; the merge kernel
+//    writes q rotated in place once every split has read it.
 //    An in-kernel merge would need device-scope release/acquire between
 //    workgroups on different XCDs (L2 writeback, counters) and a single
 //    workgroup folding a whole head's partials; measured, it saves less than
