@@ -40,6 +40,14 @@ __device__ __forceinline__ f16x8 buf_ld16(BufRsrc r, uint32_t byte_off) {
     const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
     return __builtin_bit_cast(f16x8, v);
 }
+// The same load with the non-temporal hint (cache-policy bit nt), for data
+// that is read exactly once: the decode's K/V stream reads HBM ~10 % faster
+// with it (the caches do not keep lines nobody reads again).
+__device__ __forceinline__ f16x8 buf_ld16_nt(BufRsrc r, uint32_t byte_off) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 2);
+    return __builtin_bit_cast(f16x8, v);
+}
 
 // One LDS-DMA instruction (buffer_load_dwordx4 ... lds): each lane copies 16
 // bytes at byte offset voff of the buffer described by `r` to LDS bytes

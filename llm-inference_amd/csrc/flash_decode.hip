@@ -27,23 +27,24 @@
 //    cross-lane exchange (two xor shuffles).  The waves of a workgroup merge
 //    through LDS and write one unnormalised partial (max, sum, acc[D]) per
 //    query head to the caller's workspace.
-//    K/V are read through raw buffer resources covering exactly the chunk:
-//    rows past the chunk read as zero without a memory access, so the last
-//    batch needs no clamping and the prefetch past the end is free.
+//    K/V are read once, with the non-temporal hint, through raw buffer
+//    resources covering exactly the chunk: rows past the chunk read as zero
+//    without a memory access, so the last batch needs no clamping and the
+//    prefetch past the end is free.
 //  * merge: grid = (Hq, D/4), one wave per workgroup.  Each wave folds
 //    every split's partial for 4 output dims of one head: M = max_c m_c,
 //    l = sum_c 2^(m_c-M) l_c, out = sum_c 2^(m_c-M) acc_c / l (an online merge
 //    per lane over 16-byte partial loads, then xor shuffles).
 //    The kernel boundary orders the partial writes before the merge reads.
+//    An in-kernel merge would need device-scope release/acquire between
+//    workgroups on different XCDs (L2 writeback, counters) and a single
+//    workgroup folding a whole head's partials; measured, it saves less than
+//    the second launch costs.
 //  * ROPE variants (attn_rope_store_kv_decode): the decode token's RoPE + KV
 //    append (rope.hip.cpp:61-134 for one token) folded into the two kernels:
 //    the split kernel rotates q in registers and the workgroups whose chunk
 //    holds the new row write it before reading their chunk; the merge kernel
 //    writes q rotated in place once every split has read it.
-//    An in-kernel merge would need device-scope release/acquire between
-//    workgroups on different XCDs (L2 writeback, counters) and a single
-//    workgroup folding a whole head's partials; measured, it saves less than
-//    the second launch costs.
 #include "attn_internal.hpp"
 
 #include <algorithm>
@@ -158,9 +159,9 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-            for (int s = 0; s < 4; ++s) kv.k[tt][s] = buf_ld16(rk, base + koff[tt] + 64u * s);
+            for (int s = 0; s < 4; ++s) kv.k[tt][s] = buf_ld16_nt(rk, base + koff[tt] + 64u * s);
 #pragma unroll
-        for (int r = 0; r < 8; ++r) kv.v[r] = buf_ld16(rv, base + voff[r]);
+        for (int r = 0; r < 8; ++r) kv.v[r] = buf_ld16_nt(rv, base + voff[r]);
     };
 
     f32x4 acc[8];
@@ -402,17 +403,23 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
     p.path = hpw == 4 ? 1 : hpw == 2 ? 2 : 3;
     p.block = 512;
     const uint32_t groups = num_kv_heads / hpw;       // grid.y
-    const uint32_t unit = 32u * (8u / hpw);           // one batch per wave
+    // chunks are sized in steps of 8 keys (the waves mask the keys of a
+    // partial batch): a step of one batch per wave (32 * 8/HPW keys) left up
+    // to a third of the CUs idle just past multiples of 16384 keys (L = 32769:
+    // 86 splits of 384 keys, 20.1 us, against 125 of 264 keys, 16.5 us)
+    const uint32_t unit = 8u;
     const uint32_t units = (kv_len + unit - 1) / unit;
     const uint32_t cus = (uint32_t)std::max(1, device_cu_count(device));
     const long sopt = get_option(kOptDecodeSplits);
     // one 8-wave workgroup per CU
     const uint32_t target = sopt > 0 ? (uint32_t)sopt : std::max(1u, (cus + groups - 1) / groups);
     uint32_t nsplit = std::max(1u, std::min<uint32_t>({target, units, (uint32_t)kMaxSplits}));
-    uint32_t chunk = ((units + nsplit - 1) / nsplit) * unit;
+    // at least 16 keys per split: with chunks of >= KV_CHUNK (12) keys the
+    // states fit the caller's Hq * ceil(L / 12)-state workspace
+    uint32_t chunk = std::max(16u, ((units + nsplit - 1) / nsplit) * unit);
     // a chunk's rows must fit one 32-bit buffer range
     const uint64_t max_rows = (0xffffffffull - kD * 2) / (kv_stride * 2);
-    while (chunk > max_rows && chunk > unit) chunk -= unit;
+    while (chunk > max_rows && chunk > 16u) chunk -= unit;
     nsplit = (kv_len + chunk - 1) / chunk;
     p.nsplit = nsplit;
     p.chunk = chunk;

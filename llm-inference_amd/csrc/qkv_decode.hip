@@ -59,8 +59,8 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void qkv_gemv(QkvArgs a) {
             for (int k = 0; k < kRound; ++k) {
                 const uint32_t off = (base + (lane + 64u * (uint32_t)k) * 8u) * 2u;
                 xv[k] = buf_ld16(rx, off);
-                w0[k] = buf_ld16(rw0, off);
-                w1[k] = buf_ld16(rw1, off);
+                w0[k] = buf_ld16_nt(rw0, off);  // each weight is read once per call
+                w1[k] = buf_ld16_nt(rw1, off);
             }
 #pragma unroll
             for (int k = 0; k < kRound; ++k)
