@@ -25,6 +25,11 @@ __device__ __forceinline__ f16x8 ld16(const f16* p) {
 __device__ __forceinline__ void st16(f16* p, f16x8 v) {
     *reinterpret_cast<f16x8*>(p) = v;
 }
+// The same store with the non-temporal hint (the RoPE + KV append kernel's
+// outputs: 18.0 -> 16.8 us at 8192 tokens).
+__device__ __forceinline__ void st16_nt(f16* p, f16x8 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<f16x8*>(p));
+}
 
 // Raw buffer resource over [base, base + bytes): 16-byte loads through it use
 // 32-bit offsets, and any load past `bytes` returns zeros without touching

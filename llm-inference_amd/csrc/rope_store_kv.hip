@@ -14,7 +14,8 @@
 // rotation pairs of one head = a 16-byte load from each half of the head, plus
 // the matching 16 bytes of cos and sin.  Per token the lanes cover
 // (Hq + 2*Hkv) heads x D/16 lanes, so consecutive lanes stream consecutive
-// 16-byte chunks of the [Q | K | V] rows.
+// 16-byte chunks of the [Q | K | V] rows.  Stores carry the non-temporal hint
+// (each output byte is written once).
 #include "attn_internal.hpp"
 
 namespace attn {
@@ -45,8 +46,8 @@ __global__ __launch_bounds__(256) void rope_store_kv_vec(RopeArgs a) {
         const f16x8 s = ld16(a.sin_t + pos * half + off0);
         f16x8 o0, o1;
         rope_rotate8(ld16(x + off0), ld16(x + off1), c, s, o0, o1);
-        st16(x + off0, o0);
-        st16(x + off1, o1);
+        st16_nt(x + off0, o0);
+        st16_nt(x + off1, o1);
         return;
     }
     if (slot < a.num_heads + a.num_kv_heads) {
@@ -58,13 +59,13 @@ __global__ __launch_bounds__(256) void rope_store_kv_vec(RopeArgs a) {
             const f16x8 s = ld16(a.sin_t + pos * half + off0);
             f16x8 o0, o1;
             rope_rotate8(ld16(src + off0), ld16(src + off1), c, s, o0, o1);
-            st16(dst + off0, o0);
-            st16(dst + off1, o1);
+            st16_nt(dst + off0, o0);
+            st16_nt(dst + off1, o1);
         } else {
             if (!a.kc) return;
             f16* dst = a.kc + pos * kv_dim + (uint64_t)h * D;
-            st16(dst + off0, ld16(src + off0));
-            st16(dst + off1, ld16(src + off1));
+            st16_nt(dst + off0, ld16(src + off0));
+            st16_nt(dst + off1, ld16(src + off1));
         }
         return;
     }
@@ -73,8 +74,8 @@ __global__ __launch_bounds__(256) void rope_store_kv_vec(RopeArgs a) {
     const uint32_t h = slot - a.num_heads - a.num_kv_heads;
     const f16* src = a.v + (uint64_t)t * a.k_stride + (uint64_t)h * D;
     f16* dst = a.vc + pos * kv_dim + (uint64_t)h * D;
-    st16(dst + off0, ld16(src + off0));
-    st16(dst + off1, ld16(src + off1));
+    st16_nt(dst + off0, ld16(src + off0));
+    st16_nt(dst + off1, ld16(src + off1));
 }
 
 // Generic path: any even head_dim, any strides/alignment.  One thread per
