@@ -195,6 +195,71 @@ int attn_qkv_gemm_rope_store_kv(const attn_f16_t* x, attn_f16_t* y, const attn_f
 int attn_rope_tables(attn_f16_t* cos_out, attn_f16_t* sin_out, size_t max_seq_len,
                      size_t head_dim, float rope_theta);
 
+/* ---- weights.bin: the model file the engine maps (python/export_weights.py;
+ * include/model_config.hpp, model.hpp:18-93, device_weights.hpp:57-110).
+ * Layout: the 44-byte header below; uint32 tokenizer-JSON length; the JSON;
+ * zero padding to a 64-byte file offset; then fp16 tensors back to back:
+ * embedding [vocab][hidden]; per layer input_norm [hidden], q_proj
+ * [Hq*D][hidden], k_proj [Hkv*D][hidden], v_proj [Hkv*D][hidden], (q_norm [D],
+ * k_norm [D] only if the checkpoint has them), o_proj [hidden][Hq*D],
+ * post_attention_norm [hidden], gate_proj, up_proj [inter][hidden], down_proj
+ * [hidden][inter]; final norm [hidden]; lm_head [vocab][hidden].  q_proj, k_proj
+ * and v_proj are adjacent, so q_proj is the fused [Hq*D + 2*Hkv*D][hidden] QKV
+ * weight the projections above take.  Pure host code (no HIP calls). */
+typedef struct attn_model_config {   /* model_config.hpp:10-24, 44 bytes */
+    char magic[4];                   /* "QWEN" */
+    uint32_t vocab_size, hidden_size, num_layers, num_heads, num_kv_heads, head_dim,
+        intermediate_size, max_seq_len;
+    float rms_norm_eps, rope_theta;
+} attn_model_config;
+
+/* Tensor offsets are in fp16 elements from the start of the weight payload;
+ * layer l's tensors start at layer_base + l * layer_elems + the per-layer
+ * offset.  q_norm / k_norm are UINT64_MAX when the file has none. */
+typedef struct attn_weights_layout {
+    attn_model_config config;
+    uint32_t has_qk_norm;
+    uint64_t tokenizer_offset, tokenizer_bytes;   /* JSON, file offset and length */
+    uint64_t weights_offset;     /* file offset of the payload (multiple of 64) */
+    uint64_t weights_bytes;      /* payload bytes present in the file */
+    uint64_t layout_bytes;       /* payload bytes the tensors occupy (<= weights_bytes) */
+    uint64_t embedding, final_norm, lm_head, layer_base, layer_elems;
+    uint64_t input_norm, q_proj, k_proj, v_proj, q_norm, k_norm, o_proj, post_attn_norm,
+        gate_proj, up_proj, down_proj;
+} attn_weights_layout;
+
+/* Format errors (negative; the messages are attn_weights_error_string's). */
+#define ATTN_WEIGHTS_SHORT_HEADER        (-1) /* model_config.hpp:34-35 */
+#define ATTN_WEIGHTS_BAD_MAGIC           (-2) /* model_config.hpp:39-40 */
+#define ATTN_WEIGHTS_NO_TOKENIZER_LENGTH (-3) /* model.hpp:50-52 */
+#define ATTN_WEIGHTS_TOKENIZER_TRUNCATED (-4) /* model.hpp:57-59 */
+#define ATTN_WEIGHTS_NO_PAYLOAD          (-5) /* model.hpp:84-86 */
+#define ATTN_WEIGHTS_PAYLOAD_SHORT       (-6) /* not checked by the reference */
+#define ATTN_WEIGHTS_SIZE_OVERFLOW       (-7) /* not checked by the reference */
+
+/* Parses a weights.bin of file_bytes bytes from its first head_bytes bytes
+ * (at least min(file_bytes, 48): the header and the tokenizer length; the
+ * JSON itself is not read), in the reference's order of checks
+ * (model_config.hpp:33-43, model.hpp:40-93), then lays out the payload as
+ * attn_weights_layout_for does.  Returns 0, a negative ATTN_WEIGHTS_* code, or
+ * hipErrorInvalidValue for null pointers or a short head. */
+int attn_weights_parse(const void* head, size_t head_bytes, uint64_t file_bytes,
+                       attn_weights_layout* out);
+
+/* Tensor layout of a payload of payload_bytes bytes for config (the claims of
+ * device_weights.hpp:80-109, in the exporter's order export_weights.py:89-134).
+ * Deviations, both for files the reference would read out of bounds or
+ * misread: a payload smaller than the tensors is rejected
+ * (ATTN_WEIGHTS_PAYLOAD_SHORT), and a payload of exactly the size with
+ * q_norm/k_norm per layer (export_weights.py:108-111) lays them out after
+ * v_proj (has_qk_norm = 1).  tokenizer_* and weights_offset are left 0. */
+int attn_weights_layout_for(const attn_model_config* config, uint64_t payload_bytes,
+                            attn_weights_layout* out);
+
+/* Static message for an ATTN_WEIGHTS_* code (the reference's exception texts
+ * where it has one), or NULL for an unknown code. */
+const char* attn_weights_error_string(int code);
+
 /* Introspection for tests and benchmarks: the decode plan chosen for a shape
  * on the current device.  out[0] = path (0 generic; 1, 2, 3 = MFMA split
  * kernel serving 4, 2, 1 KV heads per workgroup), out[1] = splits of the

@@ -35,6 +35,28 @@ class AttnError(RuntimeError):
     pass
 
 
+class ModelConfigC(ctypes.Structure):
+    """attn_model_config: the 44-byte weights.bin header (model_config.hpp:10-24)."""
+    _fields_ = [("magic", _c.c_char * 4)] + [
+        (f, _c.c_uint32) for f in ("vocab_size", "hidden_size", "num_layers", "num_heads",
+                                   "num_kv_heads", "head_dim", "intermediate_size",
+                                   "max_seq_len")] + [
+        ("rms_norm_eps", _c.c_float), ("rope_theta", _c.c_float)]
+
+
+WEIGHT_LAYER_FIELDS = ("input_norm", "q_proj", "k_proj", "v_proj", "q_norm", "k_norm", "o_proj",
+                       "post_attn_norm", "gate_proj", "up_proj", "down_proj")
+
+
+class WeightsLayout(ctypes.Structure):
+    """attn_weights_layout (include/attn_mi355x.h)."""
+    _fields_ = [("config", ModelConfigC), ("has_qk_norm", _c.c_uint32)] + [
+        (f, _c.c_uint64) for f in ("tokenizer_offset", "tokenizer_bytes", "weights_offset",
+                                   "weights_bytes", "layout_bytes", "embedding", "final_norm",
+                                   "lm_head", "layer_base", "layer_elems")] + [
+        (f, _c.c_uint64) for f in WEIGHT_LAYER_FIELDS]
+
+
 def _declare(lib):
     sig = {
         "attn_rope_store_kv": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz,
@@ -62,6 +84,10 @@ def _declare(lib):
         "attn_rope_store_kv_decode": (_c.c_int, [_vp] * 11 + [_sz] * 6 + [_c.c_int, _vp, _vp,
                                                                           _vp]),
         "attn_update_rope_decode_nodes": (_c.c_int, [_vp, _vp, _vp, _sz, _sz, _c.c_int]),
+        "attn_weights_parse": (_c.c_int, [_vp, _sz, _c.c_uint64, _c.POINTER(WeightsLayout)]),
+        "attn_weights_layout_for": (_c.c_int, [_c.POINTER(ModelConfigC), _c.c_uint64,
+                                               _c.POINTER(WeightsLayout)]),
+        "attn_weights_error_string": (_c.c_char_p, [_c.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -88,7 +114,8 @@ def exported_symbols():
             "attn_prefill_plan", "attn_set_option", "attn_version", "attn_qkv_decode",
             "attn_qkv_rope_store_kv_decode", "attn_update_qkv_rope_node", "attn_qkv_gemm",
             "attn_qkv_gemm_rope_store_kv", "attn_rope_store_kv_decode",
-            "attn_update_rope_decode_nodes"]
+            "attn_update_rope_decode_nodes", "attn_weights_parse", "attn_weights_layout_for",
+            "attn_weights_error_string"]
 
 
 def _ptr(x) -> Optional[int]:
@@ -284,6 +311,88 @@ class KVCache:
             raise IndexError(f"KV cache capacity exceeded: requested {n} tokens, capacity "
                              f"{self.max_seq_len}")
         self.cached_len = n
+
+
+def _weights_error(rc: int, what: str):
+    msg = lib().attn_weights_error_string(rc)
+    raise AttnError(f"{what}: " + (msg.decode() if msg else f"hipError {rc}"))
+
+
+def weights_parse(head: bytes, file_bytes: int) -> WeightsLayout:
+    """Layout of a weights.bin of file_bytes bytes from its first bytes (at least
+    48: the header and the tokenizer length); raises AttnError with the
+    reference's message on a malformed file (model.hpp:40-93)."""
+    lay = WeightsLayout()
+    buf = ctypes.create_string_buffer(bytes(head), len(head))
+    rc = lib().attn_weights_parse(ctypes.addressof(buf), len(head), file_bytes, ctypes.byref(lay))
+    if rc != 0:
+        _weights_error(rc, "attn_weights_parse")
+    return lay
+
+
+def weights_layout_for(config: ModelConfigC, payload_bytes: int) -> WeightsLayout:
+    lay = WeightsLayout()
+    rc = lib().attn_weights_layout_for(ctypes.byref(config), payload_bytes, ctypes.byref(lay))
+    if rc != 0:
+        _weights_error(rc, "attn_weights_layout_for")
+    return lay
+
+
+class ModelWeights:
+    """A weights.bin in device memory the way the engine holds it
+    (model.hpp:18-32, device_weights.hpp:57-110): the whole fp16 payload in one
+    allocation, tensors addressed by offsets into it.  `qkv(l)` is layer l's
+    fused [Hq*D + 2*Hkv*D][hidden] QKV weight (q_proj, k_proj, v_proj
+    adjacent), the matrix the QKV projections take."""
+
+    def __init__(self, path, device="cuda"):
+        path = pathlib.Path(path)
+        size = path.stat().st_size
+        with open(path, "rb") as f:
+            head = f.read(48)
+        self.layout = weights_parse(head, size)
+        lay = self.layout
+        self.config = lay.config
+        with open(path, "rb") as f:
+            f.seek(lay.tokenizer_offset)
+            self.tokenizer_json = f.read(lay.tokenizer_bytes)
+        n = lay.weights_bytes // 2
+        self.buffer = torch.empty(n, dtype=torch.float16, device=device)
+        # streamed through one 64 MiB pinned buffer: the file is never held
+        # whole in host memory; each copy completes before the buffer is reused
+        chunk = min(n, 32 << 20)
+        stage = torch.empty(chunk, dtype=torch.float16, pin_memory=True)
+        raw = memoryview(stage.numpy()).cast("B")
+        with open(path, "rb") as f:
+            f.seek(lay.weights_offset)
+            for o in range(0, n, chunk):
+                c = min(chunk, n - o)
+                got = 0
+                while got < 2 * c:
+                    r = f.readinto(raw[got:2 * c])
+                    if not r:
+                        raise AttnError(f"{path}: payload ended early")
+                    got += r
+                self.buffer[o:o + c].copy_(stage[:c])
+
+    def _view(self, offset, *shape):
+        n = math.prod(shape)
+        return self.buffer[offset:offset + n].view(*shape)
+
+    def layer(self, l, field):
+        """Offset (elements) of a per-layer tensor (WEIGHT_LAYER_FIELDS)."""
+        lay = self.layout
+        if not 0 <= l < lay.config.num_layers:
+            raise IndexError(l)
+        rel = getattr(lay, field)
+        if rel == 2**64 - 1:
+            raise KeyError(f"{field} is not in this file")
+        return lay.layer_base + l * lay.layer_elems + rel
+
+    def qkv(self, l):
+        c = self.config
+        rows = (c.num_heads + 2 * c.num_kv_heads) * c.head_dim
+        return self._view(self.layer(l, "q_proj"), rows, c.hidden_size)
 
 
 def scale(head_dim: int) -> float:

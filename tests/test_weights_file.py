@@ -1,0 +1,227 @@
+"""weights.bin, the file the engine loads its model from (python/export_weights.py,
+include/model_config.hpp, model.hpp:18-93, device_weights.hpp:57-110), as
+parsed by libattn_mi355x.so (attn_weights_parse / attn_weights_layout_for)
+and by the reference-named C++ headers (ModelConfig, MemoryMappedFile,
+DeviceWeights, Model).  Host code only.
+
+The expected tensor positions come from oracle/weights_file.py, which writes
+synthetic files in the exporter's order and records each tensor's position
+from the file offset at which it was written; the error cases are the
+reference's own checks with its exception texts, plus the two checks this
+library adds (payload shorter than its tensors, 64-bit size overflow)."""
+import pathlib
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+import weights_file as wf
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HIPCC = "/opt/rocm/bin/hipcc"
+LIB_DIR = ROOT / "llm-inference_amd" / "lib"
+
+TINY = dict(vocab_size=96, hidden_size=64, num_layers=3, num_heads=4, num_kv_heads=2,
+            head_dim=16, intermediate_size=40, max_seq_len=32, rms_norm_eps=1e-5,
+            rope_theta=10000.0)
+LAYER_NAMES = {"input_norm": "input_layernorm", "q_proj": "self_attn.q_proj",
+               "k_proj": "self_attn.k_proj", "v_proj": "self_attn.v_proj",
+               "q_norm": "self_attn.q_norm", "k_norm": "self_attn.k_norm",
+               "o_proj": "self_attn.o_proj", "post_attn_norm": "post_attention_layernorm",
+               "gate_proj": "mlp.gate_proj", "up_proj": "mlp.up_proj",
+               "down_proj": "mlp.down_proj"}
+ABSENT = 2**64 - 1
+
+
+def parse_file(attn, path, head_len=48):
+    data = pathlib.Path(path).read_bytes()
+    return attn.weights_parse(data[:head_len], len(data))
+
+
+def check_positions(lay, cfg, where, qk_norm):
+    """Every tensor the layout names sits where the writer put it."""
+    assert lay.embedding * 2 == where["model.embed_tokens.weight"][0]
+    assert lay.final_norm * 2 == where["model.norm.weight"][0]
+    assert lay.lm_head * 2 == where["lm_head.weight"][0]
+    for l in range(cfg["num_layers"]):
+        for field, hf in LAYER_NAMES.items():
+            rel = getattr(lay, field)
+            name = f"model.layers.{l}.{hf}.weight"
+            if field in ("q_norm", "k_norm") and not qk_norm:
+                assert rel == ABSENT and name not in where
+                continue
+            assert (lay.layer_base + l * lay.layer_elems + rel) * 2 == where[name][0], (l, field)
+    # the fused QKV weight: q_proj, k_proj, v_proj back to back
+    assert lay.k_proj - lay.q_proj == cfg["num_heads"] * cfg["head_dim"] * cfg["hidden_size"]
+    assert lay.v_proj - lay.k_proj == cfg["num_kv_heads"] * cfg["head_dim"] * cfg["hidden_size"]
+
+
+@pytest.mark.parametrize("tok_len", [0, 1, 15, 16, 17, 63, 64, 65, 1000])
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_layout_matches_exporter_write_order(attn, tmp_path, tok_len, qk_norm):
+    path = tmp_path / "weights.bin"
+    tok = bytes((i * 7 + 3) % 251 for i in range(tok_len))
+    base, where = wf.write(path, TINY, tok, seed=tok_len, qk_norm=qk_norm)
+    size = path.stat().st_size
+    for head_len in (48, size):
+        lay = parse_file(attn, path, head_len)
+        assert lay.weights_offset == base and base % 64 == 0
+        assert base - (48 + tok_len) < 64
+        assert (lay.tokenizer_offset, lay.tokenizer_bytes) == (48, tok_len)
+        assert lay.weights_bytes == lay.layout_bytes == size - base
+        assert lay.has_qk_norm == int(qk_norm)
+        assert lay.config.magic == b"QWEN"
+        for f in wf.CONFIG_FIELDS:
+            assert getattr(lay.config, f) == pytest.approx(TINY[f], rel=1e-7), f
+        check_positions(lay, TINY, where, qk_norm)
+
+
+def test_smollm3_3b_layout():
+    """SmolLM3-3B's file (36 layers, 2048 -> 16 x 128 / 4 x 128 heads, 11008
+    MLP, 128256 vocabulary, lm_head written as the tied embedding): the layout
+    from the header alone, against running sums over the exporter's tensor
+    list."""
+    import attn_mi355x as attn
+    cfg = wf.SMOLLM3_3B
+    c = attn.ModelConfigC(b"QWEN", *[cfg[f] for f in wf.CONFIG_FIELDS])
+    shapes = wf.tensor_shapes(cfg)
+    sizes = [int(np.prod(s)) for _, s in shapes]
+    starts = dict(zip([n for n, _ in shapes], np.concatenate([[0], np.cumsum(sizes)[:-1]])))
+    total = sum(sizes)
+    lay = attn.weights_layout_for(c, 2 * total)
+    assert lay.layout_bytes == 2 * total == 6_675_533_824
+    assert lay.has_qk_norm == 0
+    assert lay.lm_head == starts["lm_head.weight"] == 128256 * 2048 * 1 + 36 * lay.layer_elems + 2048
+    for l in (0, 1, 17, 35):
+        for field, hf in LAYER_NAMES.items():
+            if field in ("q_norm", "k_norm"):
+                continue
+            assert lay.layer_base + l * lay.layer_elems + getattr(lay, field) == \
+                starts[f"model.layers.{l}.{hf}.weight"], (l, field)
+    # the fused QKV weight of a layer is 3072 x 2048 (q_dim + 2 kv_dim rows)
+    assert lay.o_proj - lay.q_proj == 3072 * 2048
+
+
+def test_trailing_bytes_keep_the_reference_layout(attn, tmp_path):
+    """A payload longer than its tensors (not the QK-norm size) is read with
+    the plain layout, as DeviceWeights does; the extra bytes are uploaded
+    too (total_bytes is the whole remainder, model.hpp:88-92)."""
+    path = tmp_path / "w.bin"
+    base, where = wf.write(path, TINY, b"{}", trailing=b"\x01" * 10)
+    lay = parse_file(attn, path)
+    assert lay.has_qk_norm == 0
+    assert lay.weights_bytes == lay.layout_bytes + 10
+    check_positions(lay, TINY, where, False)
+
+
+def header(cfg=TINY, magic=b"QWEN"):
+    return wf.header_bytes(cfg, magic)
+
+
+@pytest.mark.parametrize("data,code", [
+    (b"", -1), (header()[:43], -1),
+    (b"QWEM" + header()[4:] + struct.pack("<I", 0) + b"\0" * 4096, -2),
+    (header(), -3), (header() + b"\x05\x00\x00", -3),
+    (header() + struct.pack("<I", 9) + b"abcd", -4),
+    (header() + struct.pack("<I", 2**32 - 1) + b"x" * 100, -4),
+    (header() + struct.pack("<I", 4) + b"abcd", -5),            # ends at the payload offset
+    (header() + struct.pack("<I", 4) + b"abcd" + b"\0" * 12, -5),  # ends inside the padding
+])
+def test_reference_format_errors(attn, data, code):
+    """The reference's checks in its order, with its messages (model_config.hpp:
+    33-43, model.hpp:49-86)."""
+    msg = attn.lib().attn_weights_error_string(code).decode()
+    with pytest.raises(attn.AttnError) as e:
+        attn.weights_parse(data[:48], len(data))
+    assert msg in str(e.value)
+
+
+def test_short_payload_is_rejected(attn, tmp_path):
+    """The reference would hand out pointers past its allocation; here the
+    file is rejected (the payload ends 2 bytes before lm_head does)."""
+    path = tmp_path / "w.bin"
+    wf.write(path, TINY, b"tok")
+    data = path.read_bytes()[:-2]
+    with pytest.raises(attn.AttnError, match="smaller than the tensors"):
+        attn.weights_parse(data[:48], len(data))
+
+
+def test_size_overflow_is_rejected(attn):
+    big = dict(TINY, vocab_size=2**32 - 1, hidden_size=2**32 - 1, num_layers=2**32 - 1,
+               intermediate_size=2**32 - 1)
+    c = attn.ModelConfigC(b"QWEN", *[big[f] for f in wf.CONFIG_FIELDS])
+    with pytest.raises(attn.AttnError, match="overflow"):
+        attn.weights_layout_for(c, 2**63)
+
+
+def test_parse_argument_checks(attn):
+    L = attn.lib()
+    lay = attn.WeightsLayout()
+    buf = header() + struct.pack("<I", 0)
+    assert L.attn_weights_parse(None, 48, 4096, attn.ctypes.byref(lay)) == 1
+    assert L.attn_weights_parse(buf, 47, 4096, attn.ctypes.byref(lay)) == 1  # head too short
+    assert L.attn_weights_parse(buf, 48, 4096, None) == 1
+    assert L.attn_weights_error_string(0) is None
+    assert L.attn_weights_error_string(-99) is None
+
+
+CPP = r'''
+#include "model.hpp"
+#include <cstdio>
+#include <cstring>
+
+int main(int argc, char** argv) {
+    // the header and the mapping, as Model's constructor reads them
+    MemoryMappedFile file(argv[1]);
+    ModelConfig cfg(file.bytes());
+    std::printf("config %u %u %u %u %u %u %u %u\n", cfg.vocab_size, cfg.hidden_size,
+                cfg.num_layers, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim,
+                cfg.intermediate_size, cfg.max_seq_len);
+    attn_weights_layout lay;
+    if (attn_weights_parse(file.bytes().data(), file.size(), file.size(), &lay) != 0) return 2;
+    std::printf("payload %llu %llu\n", (unsigned long long)lay.weights_offset,
+                (unsigned long long)lay.weights_bytes);
+    // DeviceWeights checks the payload before it allocates anything
+    try {
+        DeviceWeights w(cfg, nullptr, lay.layout_bytes - 2);
+        return 3;
+    } catch (const std::runtime_error& e) {
+        std::printf("short: %s\n", e.what());
+    }
+    // exceptions of the mapping and of the header
+    try { MemoryMappedFile missing("/nonexistent/weights.bin"); return 4; }
+    catch (const std::runtime_error& e) { std::printf("missing: %s\n", e.what()); }
+    std::byte bad[44] = {};
+    try { ModelConfig c{std::span<const std::byte>(bad, 44)}; return 5; }
+    catch (const std::runtime_error& e) { std::printf("magic: %s\n", e.what()); }
+    try { ModelConfig c{std::span<const std::byte>(bad, 43)}; return 6; }
+    catch (const std::runtime_error& e) { std::printf("size: %s\n", e.what()); }
+    return 0;
+}
+'''
+
+
+@pytest.mark.parametrize("std", ["c++20", "c++23"])
+def test_cpp_headers_parse_a_file(attn, tmp_path, std):
+    """ModelConfig, MemoryMappedFile and DeviceWeights' checks, through the
+    reference-named headers, on the host (nothing here reaches the GPU)."""
+    path = tmp_path / "weights.bin"
+    base, _ = wf.write(path, TINY, b'{"model": "tiny"}')
+    src = tmp_path / "parse.cpp"
+    src.write_text(CPP)
+    exe = tmp_path / "parse"
+    r = subprocess.run([HIPCC, f"-std={std}", "-I", str(ROOT / "include"), str(src), "-o",
+                        str(exe), "-L", str(LIB_DIR), "-lattn_mi355x", f"-Wl,-rpath,{LIB_DIR}"],
+                       capture_output=True, text=True, timeout=180)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe), str(path)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
+    lines = r.stdout.splitlines()
+    assert lines[0] == "config " + " ".join(str(TINY[f]) for f in wf.CONFIG_FIELDS[:8])
+    assert lines[1] == f"payload {base} {path.stat().st_size - base}"
+    assert lines[2] == "short: Corrupted model file: Weight payload smaller than the tensors " \
+                       "of its header"
+    assert lines[3] == "missing: File does not exist: /nonexistent/weights.bin"
+    assert lines[4] == "magic: Invalid binary file: Magic number is not 'QWEN'"
+    assert lines[5] == "size: Buffer too small for ModelConfig header (expected 44 bytes)"
