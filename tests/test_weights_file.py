@@ -225,3 +225,22 @@ def test_cpp_headers_parse_a_file(attn, tmp_path, std):
     assert lines[3] == "missing: File does not exist: /nonexistent/weights.bin"
     assert lines[4] == "magic: Invalid binary file: Magic number is not 'QWEN'"
     assert lines[5] == "size: Buffer too small for ModelConfig header (expected 44 bytes)"
+
+
+@pytest.mark.parametrize("std", ["c++20", "c++23"])
+def test_engine_uses_of_model_compile(tmp_path, std):
+    """The engine's uses of Model (src/main.cpp:19-30: construct from a mapped
+    file and return by value; model_inference.hpp:21-33: KVCache built from
+    model.config; test_qkv_gemm.cpp:56: a block's q_proj) compile against
+    these headers."""
+    src = tmp_path / "engine_uses.cpp"
+    src.write_text(
+        '#include "model.hpp"\n#include "kv_cache.hpp"\n#include "kernels/kernels.hpp"\n'
+        "Model load(const char* path) { MemoryMappedFile file(path); Model model(file);\n"
+        "  model.config.print_model_config(); return model; }\n"
+        "size_t use(const Model& model) { KVCache kv(model.config);\n"
+        "  const __half* w = model.device_weights.transformer_blocks[0].q_proj;\n"
+        "  return kv.layer_stride() + model.device_weights.total_bytes + (w != nullptr); }\n")
+    r = subprocess.run([HIPCC, f"-std={std}", "-fsyntax-only", "-I", str(ROOT / "include"),
+                        str(src)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
