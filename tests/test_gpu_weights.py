@@ -14,7 +14,8 @@ k_proj | v_proj (the GEMM on it equals the GEMM on those tensors uploaded
 separately, bit for bit); GEMM -> RoPE -> prefill on the interleaved
 [N][3072] output against the oracle; the same chain through the C++ headers
 (MemoryMappedFile + Model, tests/cpp/test_model_weights.cpp) gives the same
-bits."""
+bits; the decode step (fused QKV GEMV + RoPE + append, then Flash-Decode) on
+a loaded layer against the oracle."""
 import pathlib
 import subprocess
 
@@ -149,3 +150,57 @@ def test_cpp_model_chain(attn, gpu, loaded, model_file, tmp_path, layer):
     for suffix, mine in (("qkv", g), ("rope", rr), ("attn", out)):
         theirs = np.fromfile(f"{prefix}.{suffix}", dtype=np.uint16)
         assert np.array_equal(theirs, mine), suffix
+
+
+@pytest.mark.parametrize("layer,apply", [(0, True), (1, True), (1, False)])
+def test_decode_step_on_loaded_weights(attn, gpu, loaded, model_file, layer, apply):
+    """The engine's decode step on a loaded layer (model_inference.hpp:354-387):
+    the QKV GEMV on block.q_proj with its RoPE + KV append fused
+    (launch_qkv_rope_and_store_kv_decode), then Flash-Decode over the cache.
+    The GEMV on the loaded pointer equals the GEMV on the file's tensors bit
+    for bit; y and the new cache row equal the oracle's RoPE applied to that
+    GEMV bit for bit and the all-oracle step within tolerance; the attention
+    output is within tolerance of the fp64-softmax oracle."""
+    pos, S = 300, 320
+    print(f"[case] decode step layer={layer} apply={apply}", flush=True)
+    rng = np.random.default_rng(200 + layer)
+    x = rng.standard_normal(HIDDEN).astype(np.float16).view(np.uint16)
+    cache = rng.standard_normal(2 * S * KV_DIM).astype(np.float16).view(np.uint16)
+    cache[pos * KV_DIM:(pos + 1) * KV_DIM] = 0
+    cache[(S + pos) * KV_DIM:(S + pos + 1) * KV_DIM] = 0
+    w = file_qkv(model_file, layer)
+    cos, sin = attn.rope_tables(CFG["max_seq_len"], D, CFG["rope_theta"])
+    d_c = dev(cache, gpu)
+    kc, vc = d_c.data_ptr(), d_c.data_ptr() + 2 * S * KV_DIM
+    y = torch.empty(TOTAL, dtype=torch.float16, device=gpu)
+    attn.qkv_rope_store_kv_decode(dev(x, gpu), y, loaded.qkv(layer), kc, vc, cos.to(gpu),
+                                  sin.to(gpu), HIDDEN, HQ, HKV, D, pos, apply)
+    torch.cuda.synchronize()
+    got_y, got_c = host(y), host(d_c)
+
+    g = torch.empty(TOTAL, dtype=torch.float16, device=gpu)
+    attn.qkv_decode(dev(x, gpu), g, dev(w, gpu), HIDDEN, TOTAL)
+    torch.cuda.synchronize()
+    g = host(g)
+    c16, s16 = cos.numpy().view(np.uint16), sin.numpy().view(np.uint16)
+    q, k, v = g[:Q_DIM].copy(), g[Q_DIM:Q_DIM + KV_DIM].copy(), g[Q_DIM + KV_DIM:].copy()
+    ec = cache.copy()
+    oracle.rope_store_kv(q, k, v, ec[:S * KV_DIM], ec[S * KV_DIM:], c16, s16, 1, HQ, HKV, D,
+                         Q_DIM, KV_DIM, pos, apply)
+    assert np.array_equal(got_y, np.concatenate([q, g[Q_DIM:]])), "y vs GEMV + oracle RoPE"
+    assert np.array_equal(got_c, ec), "cache vs GEMV + oracle RoPE"
+
+    oc = cache.copy()
+    oy = oracle.qkv_rope_store_kv_decode(w, x, oc[:S * KV_DIM], oc[S * KV_DIM:], c16, s16, HQ,
+                                         HKV, D, pos, apply)
+    assert_close(got_y, oy, 2e-3, 1e-2, "y vs oracle step")
+    assert_close(got_c, oc, 2e-3, 1e-2, "cache vs oracle step")
+
+    L = pos + 1
+    out = torch.full((Q_DIM,), float("nan"), dtype=torch.float16, device=gpu)
+    po, pm, ps = attn.decode_workspace(HQ, L, D, gpu)
+    attn.decode(y, kc, vc, out, po, pm, ps, 1, L, pos, HQ, HKV, D, 0, KV_DIM)
+    torch.cuda.synchronize()
+    _, e32 = oracle.attention(got_y, got_c[:S * KV_DIM], got_c[S * KV_DIM:], 1, HQ, HKV, D, Q_DIM,
+                              KV_DIM, L, L - 1, causal=False)
+    assert_close(host(out), e32.reshape(-1), 2e-3, 1e-2, "decode vs oracle")
