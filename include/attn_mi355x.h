@@ -88,8 +88,9 @@ int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t
                 size_t num_kv_heads, size_t head_dim, size_t q_stride, size_t kv_stride,
                 hipStream_t stream, hipGraphNode_t* attention_node, hipGraphNode_t* merge_node);
 
-/* Re-point a captured decode node at a new kv_len (grid and split plan are
- * recomputed).  Replaces update_causal_attention_decode_node
+/* Re-point a captured decode node at a new kv_len (split plan, grid and the
+ * split kernel's heads-per-workgroup variant are recomputed, as a launch at
+ * that kv_len would choose them).  Replaces update_causal_attention_decode_node
  * (kernels.hpp:190-194; causal_attention.hip.cpp:975-1001). */
 int attn_update_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len);
 
@@ -277,8 +278,9 @@ int attn_prefill_plan(const void* q, const void* k, const void* v, const void* o
 
 /* Process-wide switches for tests and benchmarks (not needed in production):
  * "decode_force_generic", "decode_splits" (0 = automatic),
- * "decode_heads_per_workgroup" (0 = automatic; 1, 2 or 4 KV heads per split
- * workgroup, at most what Hkv allows), "prefill_force_generic",
+ * "decode_heads_per_workgroup" (0 = automatic: 1 up to 12288 keys, 2 above
+ * when Hkv is even; 1, 2 or 4 KV heads per split workgroup, reduced to what
+ * Hkv allows), "prefill_force_generic",
  * "qkv_gemm_force_generic", "qkv_gemm_tokens_per_wave" (0 = automatic; 32, 64
  * or 128 tokens per wave of the 256 x 128-tile MFMA GEMM), "qkv_gemm_wide"
  * (0 = automatic, from 7168 tokens; 1 = never; 2 = whenever N is a multiple

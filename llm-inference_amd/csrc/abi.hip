@@ -545,11 +545,16 @@ int attn_update_rope_decode_nodes(hipGraphExec_t graph_exec, hipGraphNode_t atte
         a.row = (uint32_t)start_pos;
         a.apply = apply_rotation ? 1u : 0u;
         if (a.apply && (!a.cos_t || !a.sin_t)) return (int)hipErrorInvalidValue;
-        replan_decode(a, device);
+        const DecodePlan p = replan_decode(a, device);
+        if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
         void* args[1] = {&a};
         params.kernelParams = args;
         params.extra = nullptr;
-        if (!m) params.gridDim.x = a.nsplit;
+        if (!m) {
+            params.func = const_cast<void*>(decode_split_symbol(p.path, true));
+            params.gridDim.x = a.nsplit;
+            params.gridDim.y = a.num_kv_heads / (p.path == 1 ? 4u : p.path == 2 ? 2u : 1u);
+        }
         e = hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
         if (e != hipSuccess) return (int)e;
     }
@@ -582,11 +587,16 @@ static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, siz
     e = hipGetDevice(&device);
     if (e != hipSuccess) return (int)e;
     a.kv_len = (uint32_t)kv_len;
-    replan_decode(a, device);
+    const DecodePlan p = replan_decode(a, device);
+    if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
     void* args[1] = {&a};
     params.kernelParams = args;
     params.extra = nullptr;
-    if (!merge) params.gridDim.x = a.nsplit;
+    if (!merge) {
+        params.func = const_cast<void*>(decode_split_symbol(p.path));
+        params.gridDim.x = a.nsplit;
+        params.gridDim.y = a.num_kv_heads / (p.path == 1 ? 4u : p.path == 2 ? 2u : 1u);
+    }
     return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
 }
 

@@ -130,9 +130,12 @@ struct DecodePlan {
 DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_heads,
                        uint32_t head_dim, uint64_t kv_stride, const void* q, const void* k,
                        const void* v, int device);
-// Recompute the split/chunk fields of an argument struct for its kv_len.
-// Used by launch and by the graph-node updaters (same plan for the same L).
-void replan_decode(DecodeArgs& a, int device);
+// Recompute the split/chunk fields of an argument struct for its kv_len and
+// return the plan, whose path (heads per workgroup) also depends on kv_len.
+// Used by launch and by the graph-node updaters (same plan for the same L):
+// an updater sets the split node's kernel to the plan's path as well as its
+// grid and arguments.
+DecodePlan replan_decode(DecodeArgs& a, int device);
 // Enqueues the split kernel and the merge kernel (two graph nodes).
 hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,
                                bool rope = false);

@@ -55,6 +55,8 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kMaxSplits = 1024;
+// longest context decoded with one KV head per workgroup (see plan_decode)
+constexpr uint32_t kOneHeadMaxKeys = 12288;
 constexpr int kAccPitch = kD + 4;
 
 struct KVBatch {
@@ -83,6 +85,9 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     const int phase = wave / HPW;
     const int n = lane & 15;   // MFMA column (query head in group) / A row
     const int gq = lane >> 4;  // MFMA k-group / output row group
+    // a grid wider than the KV heads (a graph node re-planned for another
+    // heads-per-workgroup count) has nothing for its extra workgroups
+    if (blockIdx.y * HPW >= a.num_kv_heads) return;
     const uint32_t g = blockIdx.y * HPW + hw;
     const uint32_t c = blockIdx.x;
     const uint32_t G = a.group;
@@ -392,14 +397,19 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
                          kv_stride * 2 <= 0x40000000ull && aligned16(q) && aligned16(k) &&
                          aligned16(v) && get_option(kOptDecodeForceGeneric) == 0;
     if (!mfma_ok) return p;
-    // two KV heads per workgroup when Hkv allows: measured fastest at every
-    // SmolLM3 context length (4 heads per workgroup reads whole 1 KiB cache
-    // rows but doubles the merge's partial states; 1 head streams slower)
-    uint32_t hpw = (num_kv_heads % 2 == 0) ? 2 : 1;
+    // one KV head per workgroup up to kOneHeadMaxKeys keys (SmolLM3: 3-7 %
+    // faster than two from 64 to 8192 keys -- twice the workgroups on a
+    // context that does not fill the chip), two above when Hkv allows (3-8 %
+    // faster from 16384 keys: one head per workgroup streams slower and the
+    // merge reads twice the partial states; four heads per workgroup, which
+    // read whole 1 KiB cache rows, double the states again)
+    uint32_t hpw = (num_kv_heads % 2 == 0 && kv_len > kOneHeadMaxKeys) ? 2 : 1;
+    // a forced count is reduced to what Hkv allows
     const long hopt = get_option(kOptDecodeHeadsPerGroup);
-    if (hopt == 4 && num_kv_heads % 4 == 0) hpw = 4;
-    else if (hopt == 2 && num_kv_heads % 2 == 0) hpw = 2;
-    else if (hopt == 1) hpw = 1;
+    if (hopt == 4 || hopt == 2 || hopt == 1) {
+        hpw = (uint32_t)hopt;
+        while (num_kv_heads % hpw != 0) hpw /= 2;
+    }
     p.path = hpw == 4 ? 1 : hpw == 2 ? 2 : 3;
     p.block = 512;
     const uint32_t groups = num_kv_heads / hpw;       // grid.y
@@ -427,12 +437,13 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
     return p;
 }
 
-void replan_decode(DecodeArgs& a, int device) {
+DecodePlan replan_decode(DecodeArgs& a, int device) {
     const DecodePlan p = plan_decode(a.kv_len, a.num_heads, a.num_kv_heads, a.head_dim,
                                      a.kv_stride, a.q, a.k, a.v, device);
     a.nsplit = p.nsplit;
     a.chunk = p.chunk;
     a.nstate = p.nstate;
+    return p;
 }
 
 hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,

@@ -235,14 +235,17 @@ def test_decode_graph_node_update(attn, gpu):
         hipgraph.destroy(graph, exe)
 
 
-@pytest.mark.parametrize("Hq,Hkv,hpw", [(16, 2, 0), (8, 1, 0), (16, 4, 4)])
-def test_decode_graph_node_update_other_paths(attn, gpu, Hq, Hkv, hpw):
+@pytest.mark.parametrize("Hq,Hkv,hpw,L0", [(16, 2, 0, 50), (8, 1, 0, 50), (16, 4, 4, 50),
+                                          (16, 4, 0, 19999)])
+def test_decode_graph_node_update_other_paths(attn, gpu, Hq, Hkv, hpw, L0):
     """The node patchers re-plan every split-kernel variant (4, 2 or 1 KV
-    heads per workgroup): replays equal eager launches bit for bit."""
+    heads per workgroup), including a change of variant with the context
+    length (one KV head per workgroup up to 12288 keys, two above when Hkv is
+    even), in both directions: replays equal eager launches bit for bit."""
     import ctypes
 
     from attn_mi355x import hipgraph
-    D, Lmax = 128, 9000
+    D, Lmax = 128, 20000
     rng = np.random.default_rng(Hq * 10 + Hkv)
     q = rng.standard_normal(Hq * D).astype(np.float16).view(np.uint16)
     k = rng.standard_normal(Lmax * Hkv * D).astype(np.float16).view(np.uint16)
@@ -255,12 +258,13 @@ def test_decode_graph_node_update_other_paths(attn, gpu, Hq, Hkv, hpw):
     out_g = torch.empty(Hq * D, dtype=torch.float16, device=gpu)
     out_e = torch.empty(Hq * D, dtype=torch.float16, device=gpu)
     attn.set_option("decode_heads_per_workgroup", hpw)
-    expect_path = 1 if hpw == 4 else (2 if Hkv % 2 == 0 else 3)
-    assert attn.decode_plan(Lmax, Hq, Hkv, D)["path"] == expect_path
+    for L, expect_path in ((Lmax, 1 if hpw == 4 else (2 if Hkv % 2 == 0 else 3)),
+                           (12288, 1 if hpw == 4 else 3), (12289, 1 if hpw == 4 else
+                                                           (2 if Hkv % 2 == 0 else 3))):
+        assert attn.decode_plan(L, Hq, Hkv, D)["path"] == expect_path, L
     stream = torch.cuda.Stream()
     sp = stream.cuda_stream
     anode, mnode = ctypes.c_void_p(), ctypes.c_void_p()
-    L0 = 50
     with torch.cuda.stream(stream):
         hipgraph.begin_capture(sp)
         rc = attn.lib().attn_decode(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), out_g.data_ptr(),
@@ -269,7 +273,7 @@ def test_decode_graph_node_update_other_paths(attn, gpu, Hq, Hkv, hpw):
         assert rc == 0
         graph, exe = hipgraph.end_capture(sp)
     try:
-        for L in (50, 777, 4096, 8999):
+        for L in (L0, 777, 4096, 12288, 12289, 19999, 50):
             assert attn.lib().attn_update_decode_node(exe, anode, L) == 0
             assert attn.lib().attn_update_merge_node(exe, mnode, L) == 0
             hipgraph.launch(exe, sp)
