@@ -284,7 +284,9 @@ int attn_prefill_plan(const void* q, const void* k, const void* v, const void* o
  * "qkv_gemm_force_generic", "qkv_gemm_tokens_per_wave" (0 = automatic; 32, 64
  * or 128 tokens per wave of the 256 x 128-tile MFMA GEMM), "qkv_gemm_wide"
  * (0 = automatic, from 7168 tokens; 1 = never; 2 = whenever N is a multiple
- * of 384 and Y is 16-byte aligned).  Returns 0 or -1 for an unknown name. */
+ * of 384 and Y is 16-byte aligned), "prefill_waves" (0 = automatic: 4-wave
+ * workgroups of 32 queries up to 4096 tokens, 8-wave workgroups of 64 queries
+ * above; 4 or 8 forces one).  Returns 0 or -1 for an unknown name. */
 int attn_set_option(const char* name, long value);
 
 /* Library build identification (static string). */

@@ -76,6 +76,7 @@ int attn_set_option(const char* name, long value) {
     else if (!std::strcmp(name, "qkv_gemm_force_generic")) which = kOptQkvGemmForceGeneric;
     else if (!std::strcmp(name, "qkv_gemm_tokens_per_wave")) which = kOptQkvGemmTokensPerWave;
     else if (!std::strcmp(name, "qkv_gemm_wide")) which = kOptQkvGemmWide;
+    else if (!std::strcmp(name, "prefill_waves")) which = kOptPrefillWaves;
     if (which < 0) return -1;
     g_options[which].store(value, std::memory_order_relaxed);
     return 0;

@@ -156,7 +156,7 @@ struct PrefillArgs {
     uint32_t num_kv_heads;
     uint32_t group;
     uint32_t head_dim;
-    uint32_t q_tiles;   // MFMA path: number of 64-token query tiles
+    uint32_t q_tiles;   // MFMA path: number of query tiles (set by the launcher)
     float scale_log2;
     uint32_t pad_;
 };
@@ -194,6 +194,7 @@ enum Option {
     kOptQkvGemmForceGeneric = 4,
     kOptQkvGemmTokensPerWave = 5, // 0 = automatic; 32, 64 or 128
     kOptQkvGemmWide = 6,          // 0 = automatic; 1 = never; 2 = whenever the shape allows
+    kOptPrefillWaves = 7,         // 0 = automatic; 4 or 8 waves per prefill workgroup
     kOptCount = 8
 };
 long get_option(int which);

@@ -8,7 +8,9 @@
 // MFMA path (D = 128, Hq/Hkv a multiple of 4, 16-byte aligned rows):
 //  * workgroup = 64 query tokens of 4 query heads sharing one KV head, as 8
 //    waves (two per head, 32 queries each, 2 waves per SIMD so one wave's
-//    softmax overlaps the other's MFMAs); Q, S and O stay in VGPRs.
+//    softmax overlaps the other's MFMAs); Q, S and O stay in VGPRs.  Short
+//    prompts use 32 query tokens as 4 waves (one per head and SIMD): twice
+//    the workgroups, each through its key tiles faster.
 //  * K and V of a 64-key tile are staged in LDS once per workgroup and shared
 //    by the 4 heads (the reference re-reads them per head), copied straight
 //    from global memory into LDS by buffer_load ... lds (no VGPRs, no LDS
@@ -38,10 +40,8 @@ namespace attn {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kBM = 64;        // query tokens per workgroup
+constexpr int kBM = 64;        // query tokens per workgroup, at most
 constexpr int kBN = 64;        // keys per tile
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kKP = kD + 8;    // K row pitch (halves): conflict-free 16 B A-operand reads
 // V row pitch (halves): 320-byte rows start 16 banks apart, so the 4 rows x
 // 64 bytes that 32 lanes of a transposing read address cover the 64 banks
@@ -51,7 +51,6 @@ constexpr int kKChunks = kKP / 8;             // 16-byte LDS chunks per K row (1
 constexpr int kVChunks = kVP / 8;             // ... per V row (20)
 constexpr int kKDma = kBN * kKChunks / 64;    // 1 KiB DMA instructions per K tile (17)
 constexpr int kVDma = kBN * kVChunks / 64;    // ... per V tile (20)
-constexpr int kDmaPerWave = (kVDma + kWaves - 1) / kWaves;  // 3
 
 #define LDS_AS __attribute__((address_space(3)))
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -97,7 +96,14 @@ __device__ __forceinline__ bool map_block(uint32_t bid, uint32_t quads, uint32_t
 // fp16 and the O^T accumulators are rarely touched by VALU code.
 constexpr float kRescaleSlack = 8.0f;
 
-__global__ __launch_bounds__(kThreads, 1) void prefill_d128(PrefillArgs a) {
+// WAVES = 8: 64 queries of 4 heads per workgroup, two waves per SIMD (long
+// prompts); WAVES = 4: 32 queries of 4 heads, one wave per SIMD, so a short
+// prompt's few workgroups each finish their chain of key tiles sooner.
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
+    constexpr int kW = WAVES;
+    constexpr int kBMw = 8 * WAVES;                     // query tokens per workgroup
+    constexpr int kDpw = (kVDma + WAVES - 1) / WAVES;   // DMA instructions per wave
     // two LDS buffers per operand as distinct objects, so the compiler can
     // tell a DMA into one buffer from the reads of the other
     __shared__ __attribute__((aligned(16))) f16 kt0[kBN * kKP];
@@ -114,10 +120,12 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_d128(PrefillArgs a) {
     const uint32_t quads = a.num_heads / 4u;
     uint32_t quad, tile;
     if (!map_block(blockIdx.x, quads, a.q_tiles, quad, tile)) return;
+    // the query tile's last key tile, which holds its diagonal
+    const uint32_t last = (tile * kBMw + kBMw - 1) / kBN;
     const uint32_t head = 4u * quad + (uint32_t)(wave & 3);
     const uint32_t g = (4u * quad) / a.group;
     const uint32_t N = a.seq_len;
-    const uint32_t q0 = tile * kBM + 32u * (uint32_t)(wave >> 2);  // this wave's first query
+    const uint32_t q0 = tile * kBMw + 32u * (uint32_t)(wave >> 2);  // this wave's first query
     const uint32_t q_row_bytes = (uint32_t)(a.q_stride * 2);
     const uint32_t kv_row_bytes = (uint32_t)(a.kv_stride * 2);
 
@@ -141,11 +149,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_d128(PrefillArgs a) {
     // [1024 i, 1024 i + 1024) of the buffer; lane L writes 16-byte chunk
     // q = 64 i + L = row * chunks + c, fetched from key row `row`, bytes 16c
     // (c past the row's 16 data chunks is padding: bytes 0..15 again).  Wave w
-    // issues instructions w, w + 8, w + 16.
-    uint32_t koff[kDmaPerWave], voff[kDmaPerWave];
+    // issues instructions w, w + WAVES, w + 2 WAVES, ...
+    uint32_t koff[kDpw], voff[kDpw];
 #pragma unroll
-    for (int t = 0; t < kDmaPerWave; ++t) {
-        const uint32_t q = (uint32_t)(wave + kWaves * t) * 64u + (uint32_t)lane;
+    for (int t = 0; t < kDpw; ++t) {
+        const uint32_t q = (uint32_t)(wave + kW * t) * 64u + (uint32_t)lane;
         const uint32_t kr = q / kKChunks, kc = q % kKChunks;
         const uint32_t vr = q / kVChunks, vc = q % kVChunks;
         koff[t] = kr * kv_row_bytes + (kc < 16 ? kc : 0u) * 16u;
@@ -161,8 +169,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_d128(PrefillArgs a) {
         const BufRsrc rk = make_rsrc(kbase + (uint64_t)kv0 * a.kv_stride, bytes);
         const BufRsrc rv = make_rsrc(vbase + (uint64_t)kv0 * a.kv_stride, bytes);
 #pragma unroll
-        for (int t = 0; t < kDmaPerWave; ++t) {
-            const int i = wave + kWaves * t;
+        for (int t = 0; t < kDpw; ++t) {
+            const int i = wave + kW * t;
             if (i < kKDma)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     rk, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)kt + 1024 * i), 16,
@@ -264,13 +272,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_d128(PrefillArgs a) {
         l_run += psum;
     };
 
-    // Tile t sits in buffer t & 1.  Full tiles 0..tile-1 need no mask; tile
-    // `tile` holds the diagonal.  The DMA of tile j+1 goes into the buffer
+    // Tile t sits in buffer t & 1.  Full tiles 0..last-1 need no mask; tile
+    // `last` holds the diagonal.  The DMA of tile j+1 goes into the buffer
     // last read before the previous barrier.
     stage(0, kt0, vt0);
     publish();
     uint32_t j = 0;
-    for (; j + 2 <= tile; j += 2) {
+    for (; j + 2 <= last; j += 2) {
         stage((j + 1) * kBN, kt1, vt1);
         tile_step(kt0, vt0, j, std::false_type{});
         publish();
@@ -278,13 +286,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_d128(PrefillArgs a) {
         tile_step(kt1, vt1, j + 1, std::false_type{});
         publish();
     }
-    if (j < tile) {  // j even: tile j in buffer 0, the diagonal tile j + 1 in buffer 1
+    if (j < last) {  // j even: tile j in buffer 0, the diagonal tile j + 1 in buffer 1
         stage((j + 1) * kBN, kt1, vt1);
         tile_step(kt0, vt0, j, std::false_type{});
         publish();
-        tile_step(kt1, vt1, tile, std::true_type{});
+        tile_step(kt1, vt1, last, std::true_type{});
     } else {
-        tile_step(kt0, vt0, tile, std::true_type{});
+        tile_step(kt0, vt0, last, std::true_type{});
     }
 
     // ---- epilogue: O = O^T / l, packed [N][Hq][D]
@@ -321,8 +329,20 @@ int plan_prefill(const PrefillArgs& a) {
     return 1;
 }
 
-hipError_t launch_prefill_kernel(const PrefillArgs& a, int path, hipStream_t stream) {
+// 4-wave workgroups up to this many tokens (see prefill_d128): measured 10-23 %
+// faster than 8-wave ones from 64 to 2048 tokens, 2-10 % at 4096; from 4608
+// tokens the 8-wave tile wins (27 % at 8192), its two waves per SIMD hiding
+// each other's softmax once every CU has work
+constexpr uint32_t kFourWaveMaxTokens = 4096;
+
+hipError_t launch_prefill_kernel(const PrefillArgs& a0, int path, hipStream_t stream) {
     if (path != 1) return hipErrorInvalidValue;
+    const long wopt = get_option(kOptPrefillWaves);
+    const int waves = wopt == 4 || wopt == 8 ? (int)wopt
+                                              : (a0.seq_len <= kFourWaveMaxTokens ? 4 : 8);
+    PrefillArgs a = a0;
+    const uint32_t bm = 8u * (uint32_t)waves;  // query tokens per workgroup
+    a.q_tiles = (a.seq_len + bm - 1) / bm;
     const uint32_t quads = a.num_heads / 4u;
     uint64_t blocks;
     if (quads <= 8 && (8 % quads) == 0) {
@@ -332,7 +352,10 @@ hipError_t launch_prefill_kernel(const PrefillArgs& a, int path, hipStream_t str
         blocks = (uint64_t)a.q_tiles * quads;
     }
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(prefill_d128, dim3((uint32_t)blocks), dim3(kThreads), 0, stream, a);
+    if (waves == 4)
+        hipLaunchKernelGGL(prefill_d128<4>, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(prefill_d128<8>, dim3((uint32_t)blocks), dim3(512), 0, stream, a);
     return hipGetLastError();
 }
 

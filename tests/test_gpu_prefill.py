@@ -207,3 +207,26 @@ def test_prefill_mfma_padded_strides(attn, gpu):
     torch.cuda.synchronize()
     _, e32 = oracle.attention(q, k, v, N, Hq, Hkv, D, q_stride, kv_stride, N, causal=True)
     assert_close(host(out), e32.reshape(-1), 2e-3, 1e-2, "padded strides")
+
+
+@pytest.mark.parametrize("N", [1, 31, 32, 33, 64, 65, 96, 97, 254, 1000, 1023, 1024, 2049])
+def test_prefill_four_and_eight_wave_tiles_identical(attn, gpu, N):
+    """Short prompts run 32-query workgroups of 4 waves, long ones 64-query
+    workgroups of 8 waves.  Each wave computes the same 32 queries over the
+    same key tiles in the same order either way, so the two give the same
+    bits (also past the diagonal of an odd 32-query tile and with the last
+    query tile partly past N); and both equal the oracle within tolerance."""
+    qkv, cache, stride = engine_inputs(N, seed=700 + N)
+    outs = {}
+    try:
+        for waves in (4, 8):
+            attn.set_option("prefill_waves", waves)
+            print(f"[case] prefill N={N} waves={waves}", flush=True)
+            outs[waves] = run_prefill(attn, gpu, qkv, cache, N, stride)
+    finally:
+        attn.set_option("prefill_waves", 0)
+    assert np.array_equal(outs[4], outs[8])
+    rows = None if N <= 1024 else np.unique(np.concatenate([np.arange(0, N, 7), [N - 1]]))
+    exp = oracle_prefill(qkv, cache, N, stride, rows=rows).reshape(-1)
+    got = outs[4] if rows is None else outs[4].reshape(N, -1)[rows].reshape(-1)
+    assert_close(got, exp, 2e-3, 1e-2, f"N={N}")
