@@ -1,7 +1,15 @@
-// MemoryMappedFile: read-only mapping of a model file, with the reference's
-// interface and exception texts (include/memory_mapped_file.hpp:12-95 of
-// MarcVivas/llm-inference): explicit construction from a path, move-only,
-// bytes() / size(), the file kept open and mapped until destruction.
+// MemoryMappedFile: a read-only, whole-file view of weights.bin for Model's
+// constructor.  The engine builds one from a path and hands it to Model
+// (src/main.cpp:19-30 of MarcVivas/llm-inference); only the class name and
+// the bytes() / size() accessors are that interface.
+//
+// The file is mapped once, privately and read-only.  The descriptor is closed
+// as soon as the mapping exists (a mapping outlives its descriptor), so the
+// only resource held is the mapping itself, owned by a std::unique_ptr whose
+// deleter knows the length: moves, destruction and the moved-from state come
+// from unique_ptr.  Failures throw std::runtime_error naming the path, the
+// system call and the errno text; a file shorter than the 44-byte header is
+// rejected before anything is mapped.
 #pragma once
 #include <fcntl.h>
 #include <sys/mman.h>
@@ -10,73 +18,58 @@
 
 #include <cerrno>
 #include <cstddef>
+#include <cstring>
 #include <filesystem>
+#include <memory>
 #include <span>
 #include <stdexcept>
-#include <system_error>
+#include <string>
 
 #include "model_config.hpp"
 
 class MemoryMappedFile {
 public:
     explicit MemoryMappedFile(const std::filesystem::path& path) {
-        if (!std::filesystem::exists(path))
-            throw std::runtime_error("File does not exist: " + path.string());
-        file_size = std::filesystem::file_size(path);
-        if (file_size < sizeof(ModelConfig))
-            throw std::runtime_error("File is smaller than model header");
-        fd = ::open(path.c_str(), O_RDONLY);
-        if (fd == -1) throw std::system_error(errno, std::generic_category(), "Failed to open file");
-        void* at = ::mmap(nullptr, file_size, PROT_READ, MAP_SHARED, fd, 0);
-        if (at == MAP_FAILED) {
-            const int e = errno;
+        const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+        if (fd < 0) throw failure(path, "open", errno);
+        struct stat st {};
+        if (::fstat(fd, &st) != 0) {
+            const int err = errno;
             ::close(fd);
-            fd = -1;
-            throw std::system_error(e, std::generic_category(), "Failed to mmap file");
+            throw failure(path, "fstat", err);
         }
-        // the whole file is read once, front to back, by the upload
-        ::madvise(at, file_size, MADV_WILLNEED);
-        ::madvise(at, file_size, MADV_SEQUENTIAL);
-        data = static_cast<const std::byte*>(at);
-    }
-
-    ~MemoryMappedFile() { reset(); }
-
-    MemoryMappedFile(const MemoryMappedFile&) = delete;
-    MemoryMappedFile& operator=(const MemoryMappedFile&) = delete;
-
-    MemoryMappedFile(MemoryMappedFile&& o) noexcept
-        : file_size(o.file_size), data(o.data), fd(o.fd) {
-        o.file_size = 0;
-        o.data = nullptr;
-        o.fd = -1;
-    }
-
-    MemoryMappedFile& operator=(MemoryMappedFile&& o) noexcept {
-        if (this != &o) {
-            reset();
-            file_size = o.file_size;
-            data = o.data;
-            fd = o.fd;
-            o.file_size = 0;
-            o.data = nullptr;
-            o.fd = -1;
+        const size_t length = static_cast<size_t>(st.st_size);
+        if (length < sizeof(ModelConfig)) {
+            ::close(fd);
+            throw std::runtime_error(path.string() + ": " + std::to_string(length) +
+                                     " bytes, shorter than the " +
+                                     std::to_string(sizeof(ModelConfig)) + "-byte model header");
         }
-        return *this;
+        void* at = ::mmap(nullptr, length, PROT_READ, MAP_PRIVATE, fd, 0);
+        const int err = errno;
+        ::close(fd);
+        if (at == MAP_FAILED) throw failure(path, "mmap", err);
+        // the upload reads the payload once, front to back
+        ::madvise(at, length, MADV_SEQUENTIAL);
+        mapping_ = Mapping(static_cast<const std::byte*>(at), Unmap{length});
     }
 
-    std::span<const std::byte> bytes() const noexcept { return {data, file_size}; }
-    size_t size() const noexcept { return file_size; }
+    std::span<const std::byte> bytes() const noexcept { return {mapping_.get(), size()}; }
+    size_t size() const noexcept { return mapping_ ? mapping_.get_deleter().length : 0; }
 
 private:
-    size_t file_size = 0;
-    const std::byte* data = nullptr;
-    int fd = -1;
+    struct Unmap {
+        size_t length = 0;
+        void operator()(const std::byte* p) const noexcept {
+            ::munmap(const_cast<std::byte*>(p), length);
+        }
+    };
+    using Mapping = std::unique_ptr<const std::byte, Unmap>;
+    Mapping mapping_{nullptr, Unmap{0}};
 
-    void reset() noexcept {
-        if (data) ::munmap(const_cast<std::byte*>(data), file_size);
-        data = nullptr;
-        if (fd != -1) ::close(fd);
-        fd = -1;
+    static std::runtime_error failure(const std::filesystem::path& path, const char* call,
+                                      int err) {
+        return std::runtime_error(std::string(call) + "(" + path.string() +
+                                  "): " + std::strerror(err));
     }
 };

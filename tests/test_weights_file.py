@@ -222,7 +222,7 @@ def test_cpp_headers_parse_a_file(attn, tmp_path, std):
     assert lines[1] == f"payload {base} {path.stat().st_size - base}"
     assert lines[2] == "short: Corrupted model file: Weight payload smaller than the tensors " \
                        "of its header"
-    assert lines[3] == "missing: File does not exist: /nonexistent/weights.bin"
+    assert lines[3] == "missing: open(/nonexistent/weights.bin): No such file or directory"
     assert lines[4] == "magic: Invalid binary file: Magic number is not 'QWEN'"
     assert lines[5] == "size: Buffer too small for ModelConfig header (expected 44 bytes)"
 
