@@ -75,10 +75,11 @@ int attn_prefill(const attn_f16_t* q, const attn_f16_t* k, const attn_f16_t* v,
  * and start_pos are accepted and unused, as in the reference); out is packed
  * [num_heads][head_dim].  partial_out/max/sum are caller-owned workspace of at
  * least num_heads*ceil(kv_len/ATTN_KV_CHUNK) states (partial_out: x head_dim
- * floats); their contents are private to this library.  For head_dim 128 two
- * kernels are enqueued, the split kernel (*attention_node) and the partial
- * merge (*merge_node), as in the reference; other shapes enqueue one generic
- * kernel and both handles receive it.
+ * floats); their contents are private to this library and nothing past that
+ * capacity is written.  For head_dim 128 two kernels are enqueued, the split
+ * kernel (*attention_node) and the partial merge (*merge_node), as in the
+ * reference; other shapes enqueue one generic kernel and both handles
+ * receive it.
  * Replaces launch_causal_attention_decode (kernels.hpp:104-123) and
  * launch_causal_attention_decode_vectorized (kernels.hpp:127-146;
  * causal_attention.hip.cpp:840-972). */
@@ -111,8 +112,9 @@ int attn_update_merge_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_
  * cache and out equal that pair's bit for bit.  Serves the MFMA decode path
  * (head_dim 128, 16-byte aligned tensors) with kv_stride = Hkv*D (or 0) and
  * start_pos < kv_len; other arguments return hipErrorInvalidValue and enqueue
- * nothing (use the two launches).  The node handles are the split and merge
- * kernels, patched together by attn_update_rope_decode_nodes. */
+ * nothing (issue attn_rope_store_kv and attn_decode instead).  The node
+ * handles are the split and merge kernels, patched together by
+ * attn_update_rope_decode_nodes. */
 int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16_t* v,
                               attn_f16_t* k_cache, attn_f16_t* v_cache,
                               const attn_f16_t* cos_table, const attn_f16_t* sin_table,

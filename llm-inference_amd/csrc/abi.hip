@@ -368,6 +368,27 @@ int attn_decode_plan(size_t kv_len, size_t num_heads, size_t num_kv_heads, size_
     return 0;
 }
 
+// Enqueue an MFMA decode plan as the reference does: the split kernel
+// (*attention_node) then the merge kernel (*merge_node).
+static int enqueue_decode(DecodeArgs& a, int device, bool rope, hipStream_t stream,
+                          hipGraphNode_t* attention_node, hipGraphNode_t* merge_node) {
+    const DecodePlan p = replan_decode(a, device);
+    if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
+    hipError_t e = launch_decode_split(a, p, stream, rope);
+    if (e != hipSuccess) return (int)e;
+    if (attention_node) {
+        e = captured_node(stream, attention_node);
+        if (e != hipSuccess) return (int)e;
+    }
+    e = launch_decode_merge(a, stream, rope);
+    if (e != hipSuccess) return (int)e;
+    if (merge_node) {
+        e = captured_node(stream, merge_node);
+        if (e != hipSuccess) return (int)e;
+    }
+    return 0;
+}
+
 int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t* v_cache,
                 attn_f16_t* out, float* partial_out, float* partial_max, float* partial_sum,
                 size_t query_len, size_t kv_len, size_t start_pos, size_t num_heads,
@@ -388,7 +409,6 @@ int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t
     const DecodePlan p = plan_decode((uint32_t)kv_len, (uint32_t)num_heads,
                                      (uint32_t)num_kv_heads, (uint32_t)head_dim, kvs, q,
                                      k_cache, v_cache, device);
-    hipGraphNode_t node = nullptr;
     if (p.path == 0) {
         // one kernel: both node handles name it (the merge patcher is a no-op)
         GenericAttnArgs g{};
@@ -408,6 +428,7 @@ int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t
         e = launch_generic_attention(g, stream);
         if (e != hipSuccess) return (int)e;
         if (attention_node || merge_node) {
+            hipGraphNode_t node = nullptr;
             e = captured_node(stream, &node);
             if (e != hipSuccess) return (int)e;
             if (attention_node) *attention_node = node;
@@ -431,22 +452,7 @@ int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t
     a.group = (uint32_t)(num_heads / num_kv_heads);
     a.head_dim = (uint32_t)head_dim;
     a.scale_log2 = scale_log2_for(head_dim);
-    a.nsplit = p.nsplit;
-    a.chunk = p.chunk;
-    a.nstate = p.nstate;
-    e = launch_decode_split(a, p, stream);
-    if (e != hipSuccess) return (int)e;
-    if (attention_node) {
-        e = captured_node(stream, attention_node);
-        if (e != hipSuccess) return (int)e;
-    }
-    e = launch_decode_merge(a, stream);
-    if (e != hipSuccess) return (int)e;
-    if (merge_node) {
-        e = captured_node(stream, merge_node);
-        if (e != hipSuccess) return (int)e;
-    }
-    return 0;
+    return enqueue_decode(a, device, false, stream, attention_node, merge_node);
 }
 
 int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16_t* v,
@@ -471,7 +477,9 @@ int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16
     const size_t kvs = kv_stride ? kv_stride : kv_dim;
     // the fused kernels serve the MFMA decode path with the engine's cache
     // layout (RoPE writes rows kv_dim apart, rope.hip.cpp:110) and the new
-    // token inside the decoded range; other calls use the two launches
+    // token inside the decoded range; other shapes are rejected
+    // (hipErrorInvalidValue, nothing enqueued): a caller issues
+    // attn_rope_store_kv and attn_decode for them
     if (kvs != kv_dim || start_pos >= kv_len) return (int)hipErrorInvalidValue;
     const bool al = ((uintptr_t)k | (uintptr_t)v | (uintptr_t)cos_table | (uintptr_t)sin_table |
                      (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0;
@@ -497,9 +505,6 @@ int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16
     a.group = (uint32_t)(num_heads / num_kv_heads);
     a.head_dim = (uint32_t)head_dim;
     a.scale_log2 = scale_log2_for(head_dim);
-    a.nsplit = p.nsplit;
-    a.chunk = p.chunk;
-    a.nstate = p.nstate;
     a.q_rot = reinterpret_cast<f16*>(q);
     a.k_dst = reinterpret_cast<f16*>(k_cache);
     a.v_dst = reinterpret_cast<f16*>(v_cache);
@@ -509,19 +514,33 @@ int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16
     a.sin_t = reinterpret_cast<const f16*>(sin_table);
     a.row = (uint32_t)start_pos;
     a.apply = apply_rotation ? 1u : 0u;
-    e = launch_decode_split(a, p, stream, true);
-    if (e != hipSuccess) return (int)e;
-    if (attention_node) {
-        e = captured_node(stream, attention_node);
-        if (e != hipSuccess) return (int)e;
-    }
-    e = launch_decode_merge(a, stream, true);
-    if (e != hipSuccess) return (int)e;
-    if (merge_node) {
-        e = captured_node(stream, merge_node);
-        if (e != hipSuccess) return (int)e;
-    }
-    return 0;
+    return enqueue_decode(a, device, true, stream, attention_node, merge_node);
+}
+
+// Re-point a captured split node at kv_len: its kernel (heads per
+// workgroup), grid and arguments.
+static hipError_t replan_split_node(hipGraphExec_t graph_exec, hipGraphNode_t node,
+                                    hipKernelNodeParams& params, DecodeArgs& a, bool rope,
+                                    int device) {
+    const DecodePlan p = replan_decode(a, device);
+    if (p.path < 1 || p.path > 3) return hipErrorInvalidValue;
+    void* args[1] = {&a};
+    params.kernelParams = args;
+    params.extra = nullptr;
+    params.func = const_cast<void*>(decode_split_symbol(p.path, rope));
+    params.gridDim = decode_grid(a, p);
+    return hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
+}
+
+// Re-point a captured merge node at kv_len (its split count).
+static hipError_t replan_merge_node(hipGraphExec_t graph_exec, hipGraphNode_t node,
+                                    hipKernelNodeParams& params, DecodeArgs& a, int device) {
+    const DecodePlan p = replan_decode(a, device);
+    if (p.path < 1 || p.path > 3) return hipErrorInvalidValue;
+    void* args[1] = {&a};
+    params.kernelParams = args;
+    params.extra = nullptr;
+    return hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
 }
 
 int attn_update_rope_decode_nodes(hipGraphExec_t graph_exec, hipGraphNode_t attention_node,
@@ -537,26 +556,15 @@ int attn_update_rope_decode_nodes(hipGraphExec_t graph_exec, hipGraphNode_t atte
         e = hipGraphKernelNodeGetParams(node, &params);
         if (e != hipSuccess) return (int)e;
         const bool ok = m ? params.func == decode_merge_symbol(true)
-                          : (params.func == decode_split_symbol(1, true) ||
-                             params.func == decode_split_symbol(2, true) ||
-                             params.func == decode_split_symbol(3, true));
+                          : decode_path_of_symbol(params.func, true) != 0;
         if (!ok) return (int)hipErrorInvalidValue;
         DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(params.kernelParams[0]);
         a.kv_len = (uint32_t)kv_len;
         a.row = (uint32_t)start_pos;
         a.apply = apply_rotation ? 1u : 0u;
         if (a.apply && (!a.cos_t || !a.sin_t)) return (int)hipErrorInvalidValue;
-        const DecodePlan p = replan_decode(a, device);
-        if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
-        void* args[1] = {&a};
-        params.kernelParams = args;
-        params.extra = nullptr;
-        if (!m) {
-            params.func = const_cast<void*>(decode_split_symbol(p.path, true));
-            params.gridDim.x = a.nsplit;
-            params.gridDim.y = a.num_kv_heads / (p.path == 1 ? 4u : p.path == 2 ? 2u : 1u);
-        }
-        e = hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
+        e = m ? replan_merge_node(graph_exec, node, params, a, device)
+              : replan_split_node(graph_exec, node, params, a, true, device);
         if (e != hipSuccess) return (int)e;
     }
     return 0;
@@ -578,9 +586,7 @@ static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, siz
         params.extra = nullptr;
         return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
     }
-    const bool is_split = params.func == decode_split_symbol(1) ||
-                          params.func == decode_split_symbol(2) ||
-                          params.func == decode_split_symbol(3);
+    const bool is_split = decode_path_of_symbol(params.func, false) != 0;
     const bool is_merge = params.func == decode_merge_symbol();
     if ((merge && !is_merge) || (!merge && !is_split)) return (int)hipErrorInvalidValue;
     DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(params.kernelParams[0]);
@@ -588,17 +594,8 @@ static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, siz
     e = hipGetDevice(&device);
     if (e != hipSuccess) return (int)e;
     a.kv_len = (uint32_t)kv_len;
-    const DecodePlan p = replan_decode(a, device);
-    if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
-    void* args[1] = {&a};
-    params.kernelParams = args;
-    params.extra = nullptr;
-    if (!merge) {
-        params.func = const_cast<void*>(decode_split_symbol(p.path));
-        params.gridDim.x = a.nsplit;
-        params.gridDim.y = a.num_kv_heads / (p.path == 1 ? 4u : p.path == 2 ? 2u : 1u);
-    }
-    return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
+    return (int)(merge ? replan_merge_node(graph_exec, node, params, a, device)
+                       : replan_split_node(graph_exec, node, params, a, false, device));
 }
 
 int attn_update_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len) {

@@ -120,11 +120,14 @@ struct DecodeArgs {
 };
 
 struct DecodePlan {
-    int path;          // 0 = generic (any D, any stride); 1/2/3 = MFMA split with 4/2/1 KV heads per workgroup + merge
+    // 0 = generic (any D, any stride); 1/2/3 = MFMA split kernel with 4/2/1 KV
+    // heads per workgroup + merge kernel
+    int path;
     uint32_t nsplit;
     uint32_t chunk;
     uint32_t nstate;   // partial states per query head written to the workspace
     uint32_t block;    // threads per split workgroup
+    uint32_t groups;   // KV-head groups (grid of the split workgroups: nsplit x groups)
 };
 
 DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_heads,
@@ -136,12 +139,15 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
 // an updater sets the split node's kernel to the plan's path as well as its
 // grid and arguments.
 DecodePlan replan_decode(DecodeArgs& a, int device);
-// Enqueues the split kernel and the merge kernel (two graph nodes).
+int decode_hpw(int path);                        // KV heads per split workgroup (0: generic)
+dim3 decode_grid(const DecodeArgs& a, const DecodePlan& p);  // the split kernel's grid
+// Enqueues the split kernel (followed by launch_decode_merge).
 hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,
                                bool rope = false);
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream, bool rope = false);
 const void* decode_split_symbol(int path, bool rope = false);
 const void* decode_merge_symbol(bool rope = false);
+int decode_path_of_symbol(const void* fn, bool rope);  // 0 when not a split kernel
 
 // ------------------------------------------------------------- prefill
 struct PrefillArgs {

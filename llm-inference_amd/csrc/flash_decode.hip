@@ -6,45 +6,48 @@
 // visible; for query head h the KV head is h / (Hq/Hkv); out = softmax(q.K^T /
 // sqrt(D)) V in fp32, rounded to fp16.
 //
-// Two kernels, as in the reference (attention node + merge node):
-//  * split: grid = (nsplit, Hkv/HPW).  An 8-wave workgroup owns one
-//    contiguous chunk of keys for HPW KV heads (8/HPW waves each; HPW = 2 by
-//    default, so a workgroup reads 512-byte segments of each cache row), and
-//    each wave serves ALL query heads of its group: every K/V byte is read
-//    from HBM exactly once (the reference reads it once per query head).
-//    Each wave walks its keys in rounds of two 32-key batches whose 32 loads
-//    are all issued before the round's first MFMA.
-//    Scores come from MFMA v_mfma_f32_16x16x32_f16 as S^T = K . Q^T (keys =
-//    rows, the <= 16 grouped query heads = columns): 16-byte K loads are
-//    already in A-operand layout.  The S^T key rows are permuted so that lane
-//    (gq, n) ends up holding query n and keys 8gq..8gq+7 of the batch, which
-//    is exactly the B-operand layout of P^T for the PV product.
-//    PV is O^T = V^T . P^T on the same MFMA.  Lane (gq, n) loads 16 B of V
+// The context of each KV head is cut into `nsplit` chunks.  A split
+// workgroup (8 waves) owns one chunk for HPW KV heads (HPW = 1 up to 12288
+// keys, 2 above for SmolLM3); 8/HPW waves share a KV head and each wave
+// serves ALL query heads of its group, so every K/V byte is read from HBM
+// exactly once (the reference reads it once per query head).
+//  * Scores come from v_mfma_f32_16x16x32_f16 as S^T = K . Q^T (keys = rows,
+//    the <= 16 grouped query heads = columns): 16-byte K loads are already
+//    in A-operand layout.  The S^T key rows are permuted so that lane (gq, n)
+//    ends up holding query n and keys 8gq..8gq+7 of a 32-key batch, which is
+//    exactly the B-operand layout of P^T for the PV product.
+//  * PV is O^T = V^T . P^T on the same MFMA.  Lane (gq, n) loads 16 B of V
 //    rows 8gq..8gq+7 at dims 8n..8n+7 (256 B coalesced rows) and transposes
 //    the 8x8 block in registers; MFMA tile mt covers dims {8n + mt}, so no
-//    LDS round trip is needed, and the O^T accumulator of lane (gq, n) holds
-//    query n, dims 32gq..32gq+31: only the per-query max and sum need
-//    cross-lane exchange (two xor shuffles).  The waves of a workgroup merge
-//    through LDS and write one unnormalised partial (max, sum, acc[D]) per
-//    query head to the caller's workspace.
-//    K/V are read once, with the non-temporal hint, through raw buffer
-//    resources covering exactly the chunk: rows past the chunk read as zero
-//    without a memory access, so the last batch needs no clamping and the
-//    prefetch past the end is free.
-//  * merge: grid = (Hq, D/4), one wave per workgroup.  Each wave folds
-//    every split's partial for 4 output dims of one head: M = max_c m_c,
-//    l = sum_c 2^(m_c-M) l_c, out = sum_c 2^(m_c-M) acc_c / l (an online merge
-//    per lane over 16-byte partial loads, then xor shuffles).
-//    The kernel boundary orders the partial writes before the merge reads.
-//    An in-kernel merge would need device-scope release/acquire between
-//    workgroups on different XCDs (L2 writeback, counters) and a single
-//    workgroup folding a whole head's partials; measured, it saves less than
-//    the second launch costs.
+//    LDS round trip is needed, and only the per-query max and sum need
+//    cross-lane exchange (two xor shuffles).  The softmax denominator sums
+//    the fp16-rounded P that the PV product multiplies.
+//  * K/V are read with the non-temporal hint through raw buffer resources
+//    covering exactly the chunk: rows past the chunk read as zero without a
+//    memory access, so the last batch needs no clamping and a prefetch past
+//    the end is free.  Each wave keeps two 32-key batches in flight: the
+//    loads of batch i + 2 are issued as soon as batch i has been consumed.
+//  * The waves of a workgroup fold their (max, sum, acc) through LDS into
+//    one unnormalised partial state per query head.
+//
+// Two kernels, as in the reference (attention node + merge node): the split
+// kernel above writes each workgroup's partial states to the caller's
+// workspace, the merge kernel (grid (Hq, D/4), one wave per workgroup) folds
+// every split's partial for 4 output dims of one head: M = max_c m_c,
+// l = sum_c 2^(m_c-M) l_c, out = sum_c 2^(m_c-M) acc_c / l.  The kernel
+// boundary orders the partial writes before the merge reads.  Measured and
+// rejected: one kernel holding the split workgroups and merge workgroups
+// (dispatched last) that exchange the partial states through device-coherent
+// stores and loads across XCDs -- with a per-split flag (17.3 us per call at
+// L = 32768, against 16.5 us for the two kernels), with tagged state words
+// polled directly (22.5 us), with system-scope polls (23.3 us): each step of
+// the exchange costs a ~1 us memory round trip after the last K/V byte, as
+// much as the second launch.
 //  * ROPE variants (attn_rope_store_kv_decode): the decode token's RoPE + KV
 //    append (rope.hip.cpp:61-134 for one token) folded into the two kernels:
 //    the split kernel rotates q in registers and the workgroups whose chunk
 //    holds the new row write it before reading their chunk; the merge kernel
-//    writes q rotated in place once every split has read it.
+//    writes q rotated in place once every split workgroup has read it.
 #include "attn_internal.hpp"
 
 #include <algorithm>
@@ -58,19 +61,47 @@ constexpr int kMaxSplits = 1024;
 // longest context decoded with one KV head per workgroup (see plan_decode)
 constexpr uint32_t kOneHeadMaxKeys = 12288;
 constexpr int kAccPitch = kD + 4;
+// cache-policy bit nt (non-temporal) of raw buffer loads
+constexpr int kNT = 2;
 
 struct KVBatch {
     f16x8 k[2][4];
     f16x8 v[8];
 };
 
-// HPW KV heads per 8-wave workgroup (4 for SmolLM3): wave w serves KV head
-// HPW*blockIdx.y + w % HPW and every (8/HPW)-th batch of the chunk, so the
-// waves of a workgroup read whole cache rows (all KV heads of a token)
-// together.  With one 8-wave workgroup per CU and two batches per wave, every
-// load of the kernel is issued at its start.
+template <int AUX>
+__device__ __forceinline__ float buf_ldf(BufRsrc r, uint32_t byte_off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, AUX));
+}
+template <int AUX>
+__device__ __forceinline__ f32x4 buf_ldf4(BufRsrc r, uint32_t byte_off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, AUX));
+}
+// every store this lane issued has completed; "memory" keeps the compiler
+// from moving stores across
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// q head h rotated in place by lanes 0..7 of the calling threads (lane e:
+// pairs 8e..8e+7 and their partners 64 + 8e..), as launch_rope_and_store_kv
+// leaves it
+__device__ __forceinline__ void rotate_q_head(const DecodeArgs& a, uint32_t h, uint32_t e) {
+    const uint32_t c8 = 8u * e;
+    f16* qh = a.q_rot + (uint64_t)h * kD;
+    f16x8 x0 = ld16(qh + c8), x1 = ld16(qh + 64 + c8);
+    rope_rotate8(x0, x1, ld16(a.cos_t + (uint64_t)a.row * (kD / 2) + c8),
+                 ld16(a.sin_t + (uint64_t)a.row * (kD / 2) + c8), x0, x1);
+    st16(qh + c8, x0);
+    st16(qh + 64 + c8, x1);
+}
+
+// The split kernel: grid (nsplit, Hkv / HPW); workgroup (c, grp) owns chunk c
+// of KV heads HPW*grp .. HPW*grp + HPW-1.  Wave w serves KV head
+// HPW*grp + w % HPW and every (8/HPW)-th batch of the chunk, so the waves of a
+// workgroup read whole cache-row segments together.
 template <int HPW, bool ROPE>
 __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
+    const uint32_t c = blockIdx.x;
+    const uint32_t grp = blockIdx.y;
     constexpr int WAVES = 8;
     constexpr int kThreads = WAVES * 64;
     constexpr int kPhases = WAVES / HPW;  // waves sharing one KV head
@@ -87,9 +118,8 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     const int gq = lane >> 4;  // MFMA k-group / output row group
     // a grid wider than the KV heads (a graph node re-planned for another
     // heads-per-workgroup count) has nothing for its extra workgroups
-    if (blockIdx.y * HPW >= a.num_kv_heads) return;
-    const uint32_t g = blockIdx.y * HPW + hw;
-    const uint32_t c = blockIdx.x;
+    if (grp * HPW >= a.num_kv_heads) return;
+    const uint32_t g = grp * HPW + hw;
     const uint32_t G = a.group;
     const uint32_t t0 = c * a.chunk;
     const uint32_t nk = min(a.chunk, a.kv_len - t0);  // keys in this split (>= 1)
@@ -100,28 +130,30 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     const BufRsrc rk = make_rsrc(a.k + (uint64_t)t0 * a.kv_stride + (uint64_t)g * kD, span);
     const BufRsrc rv = make_rsrc(a.v + (uint64_t)t0 * a.kv_stride + (uint64_t)g * kD, span);
 
-    // Q^T as the B operand: lane (gq, n) holds Q[g*G + n][32s + 8gq .. +7].
-    f16x8 qb[4];
-    if ((uint32_t)n < G) {
-        const f16* qp = a.q + (uint64_t)(g * G + n) * kD + 8 * gq;
+    // S^T row m of tile tt is key 8*(m/4) + 4*tt + (m%4) of the batch, so the
+    // output of lane group gq is keys 8gq + (4tt + i).
+    const uint32_t krow = 8u * (uint32_t)(n >> 2) + (uint32_t)(n & 3);
+    uint32_t koff[2], voff[8];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) qb[s] = ld16(qp + 32 * s);
-        if constexpr (ROPE) {
-            // dims 32s + 8gq + i (s = 0, 1) pair with 64 more (s + 2): the lane
-            // holds both halves of 16 rotation pairs (rope.hip.cpp:44-58)
-            if (a.apply) {
-                const f16* ct = a.cos_t + (uint64_t)a.row * (kD / 2) + 8 * gq;
-                const f16* st = a.sin_t + (uint64_t)a.row * (kD / 2) + 8 * gq;
+    for (int tt = 0; tt < 2; ++tt) koff[tt] = (krow + 4u * tt) * row_bytes + 16u * gq;
 #pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    rope_rotate8(qb[s], qb[s + 2], ld16(ct + 32 * s), ld16(st + 32 * s), qb[s],
-                                 qb[s + 2]);
-            }
-        }
-    } else {
+    for (int r = 0; r < 8; ++r) voff[r] = (8u * gq + r) * row_bytes + 16u * n;
+
+    auto load = [&](uint32_t b, KVBatch& kv) {
+        const uint32_t base = b * row_bytes;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) qb[s] = f16x8{};
-    }
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                kv.k[tt][s] = __builtin_bit_cast(
+                    f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(base + koff[tt] + 64u * s),
+                                                                 0, kNT));
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+            kv.v[r] = __builtin_bit_cast(
+                f16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, (int)(base + voff[r]), 0, kNT));
+    };
+
     if constexpr (ROPE) {
         // the workgroups whose chunk holds the new token's row append it
         // (K rotated, V copied) and only then read the chunk: the stores are
@@ -145,95 +177,130 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
                     st16(a.v_dst + dst + c16 + 8, ld16(a.v_src + src + c16 + 8));
                 }
             }
-            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the row is written
+            wait_stores();
             __syncthreads();
         }
     }
 
-    // S^T row m of tile tt is key 8*(m/4) + 4*tt + (m%4) of the batch, so the
-    // output of lane group gq is keys 8gq + (4tt + i).
-    const uint32_t krow = 8u * (uint32_t)(n >> 2) + (uint32_t)(n & 3);
-    uint32_t koff[2], voff[8];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) koff[tt] = (krow + 4u * tt) * row_bytes + 16u * gq;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) voff[r] = (8u * gq + r) * row_bytes + 16u * n;
-
-    auto load = [&](uint32_t b, KVBatch& kv) {
-        const uint32_t base = b * row_bytes;
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int s = 0; s < 4; ++s) kv.k[tt][s] = buf_ld16_nt(rk, base + koff[tt] + 64u * s);
-#pragma unroll
-        for (int r = 0; r < 8; ++r) kv.v[r] = buf_ld16_nt(rv, base + voff[r]);
-    };
-
     f32x4 acc[8];
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY;
+    // running max: a finite floor, so a wave whose batches all lie past the
+    // chunk keeps weight 2^(x - m) = 0 for its masked (-inf) keys and
+    // rescale factor 1 without special cases
+    float m_run = -1.0e30f;
     float l_run = 0.f;
-
-    // one 32-key batch: scores, online softmax, PV
-    auto compute = [&](const KVBatch& kv, uint32_t b) {
-        f32x4 st[2];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            st[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-                st[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv.k[tt][s], qb[s], st[tt], 0, 0, 0);
-        }
-        // scores of query n for keys b + 8gq + r, r = 4tt + i (log2 domain)
-        float x[8];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t key = b + 8u * gq + 4u * tt + i;
-                const float v = (key < nk) ? st[tt][i] * a.scale_log2 : -INFINITY;
-                x[4 * tt + i] = v;
-                mx = fmaxf(mx, v);
-            }
-        mx = fmaxf(mx, xor_lane(mx, 16));
-        mx = fmaxf(mx, xor_lane(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = fast_exp2(m_run - m_new);
-        f16x8 pb;
-        float psum = 0.f;
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const float p = fast_exp2(x[r] - m_new);
-            pb[r] = (f16)p;
-            psum += p;
-        }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int mt = 0; mt < 8; ++mt) {
-            acc[mt] *= alpha;
-            f16x8 va;
-#pragma unroll
-            for (int r = 0; r < 8; ++r) va[r] = kv.v[r][mt];
-            acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, acc[mt], 0, 0, 0);
-        }
-    };
-
-    // rounds of two batches: all 32 loads of a round are issued before its
-    // first MFMA, and no load stays pending across the loop back-edge (so
-    // the compiler's waits are exact: vmcnt(16) before A, vmcnt(0) before B).
-    // Rows past the chunk read zeros for free.
     constexpr uint32_t kStep = 32u * kPhases;
-    for (uint32_t b = 32u * phase; b < nk; b += 2 * kStep) {
+    uint32_t b = 32u * phase;
+    // wave-uniform: a wave whose first batch lies past the chunk (short
+    // contexts) has no keys and goes straight to the fold
+    if (b < nk) {
+        // Q^T as the B operand: lane (gq, n) holds Q[g*G + n][32s + 8gq .. +7].
+        // Q (and the rotation's cos/sin) are loaded before the first K/V batch so
+        // that the in-order load counter never makes a batch wait for them.
+        const bool qlane = (uint32_t)n < G;
+        f16x8 qb[4], rc[2], rs[2];
+        if (qlane) {
+            const f16* qp = a.q + (uint64_t)(g * G + n) * kD + 8 * gq;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) qb[s] = ld16(qp + 32 * s);
+            if constexpr (ROPE) {
+                const f16* ct = a.cos_t + (uint64_t)a.row * (kD / 2) + 8 * gq;
+                const f16* st = a.sin_t + (uint64_t)a.row * (kD / 2) + 8 * gq;
+                if (a.apply) {
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        rc[s] = ld16(ct + 32 * s);
+                        rs[s] = ld16(st + 32 * s);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) qb[s] = f16x8{};
+        }
+
+        // the first two batches of this wave
         KVBatch A, B;
         load(b, A);
         load(b + kStep, B);
-        // keep the scheduler from sinking the loads toward their uses
+
+        if constexpr (ROPE) {
+            // dims 32s + 8gq + i (s = 0, 1) pair with 64 more (s + 2): the lane
+            // holds both halves of 16 rotation pairs (rope.hip.cpp:44-58)
+            if (qlane && a.apply) {
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    rope_rotate8(qb[s], qb[s + 2], rc[s], rs[s], qb[s], qb[s + 2]);
+            }
+        }
+
+        const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
+
+        // one 32-key batch: scores, online softmax, PV
+        auto compute = [&](const KVBatch& kv, uint32_t bb) {
+            f32x4 st[2];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                st[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    st[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv.k[tt][s], qb[s], st[tt], 0, 0, 0);
+            }
+            // scores of query n for keys bb + 8gq + r, r = 4tt + i (log2 domain)
+            float x[8];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t key = bb + 8u * gq + 4u * tt + i;
+                    const float v = (key < nk) ? st[tt][i] * a.scale_log2 : -INFINITY;
+                    x[4 * tt + i] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, xor_lane(mx, 16));
+            mx = fmaxf(mx, xor_lane(mx, 32));
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = fast_exp2(m_run - m_new);
+            f16x8 pb;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) pb[r] = (f16)fast_exp2(x[r] - m_new);
+            // the denominator sums the fp16 weights the PV product uses
+            float psum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                psum = __builtin_amdgcn_fdot2(f16x2{pb[2 * r], pb[2 * r + 1]}, one2, psum, false);
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+#pragma unroll
+            for (int mt = 0; mt < 8; ++mt) {
+                acc[mt] *= alpha;
+                f16x8 va;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) va[r] = kv.v[r][mt];
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, acc[mt], 0, 0, 0);
+            }
+        };
+
+        // Batches b, b + kStep, b + 2 kStep, ... of this wave; two in flight:
+        // the loads of batch i + 2 go out once batch i is consumed.  Every path
+        // into the loop test has exactly batches A and B in flight (the last
+        // pair is peeled off below), so the compiler's waits stay vmcnt(16) for
+        // A and let B's loads overlap A's compute.
+        while (b + 2 * kStep < nk) {
+            __builtin_amdgcn_sched_barrier(0);
+            compute(A, b);
+            load(b + 2 * kStep, A);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(B, b + kStep);
+            load(b + 3 * kStep, B);
+            b += 2 * kStep;
+        }
         __builtin_amdgcn_sched_barrier(0);
         compute(A, b);
-        compute(B, b + kStep);  // keys past the chunk are masked (p = 0)
+        __builtin_amdgcn_sched_barrier(0);
+        if (b + kStep < nk) compute(B, b + kStep);  // keys past the chunk are masked (p = 0)
     }
 
     // per-query sum over the four lane groups (the max is already shared)
@@ -262,11 +329,11 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
 #pragma unroll
         for (int ph = 0; ph < kPhases; ++ph) {
             const int w = hl + HPW * ph;
-            const float wt = fast_exp2(s_m[w][qn] - M);  // idle waves: 2^-inf = 0
+            const float wt = fast_exp2(s_m[w][qn] - M);  // waves without keys: 0
             num += wt * s_acc[w][qn][d];
             den += wt * s_l[w][qn];
         }
-        const uint64_t st = (uint64_t)((blockIdx.y * HPW + hl) * G + qn) * a.nstate + c;
+        const uint64_t st = (uint64_t)((grp * HPW + hl) * G + qn) * a.nstate + c;
         a.part_out[st * kD + d] = num;
         if (d == 0) {
             a.part_max[st] = M;
@@ -278,18 +345,11 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
 constexpr int kMergeDims = 4;    // output dims per merge workgroup (one wave)
 constexpr int kMergeRound = 4;   // splits per lane per round of loads
 
-__device__ __forceinline__ float buf_ldf(BufRsrc r, uint32_t byte_off) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 0));
-}
-__device__ __forceinline__ f32x4 buf_ldf4(BufRsrc r, uint32_t byte_off) {
-    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
-}
-
-// grid (Hq, D/4), one wave per workgroup.  Lane j folds the partials of
-// splits j, j + 64, ... for 4 output dims of one head with an online merge
-// (all loads of a round issued first, through range-checked buffer
-// resources: splits past nstate read as zero and get weight 0); the 64 lanes
-// then combine with xor shuffles -- no LDS, no barrier.
+// The merge kernel: grid (Hq, D/4), one wave per workgroup.  Lane j
+// folds the partials of splits j, j + 64, ... for 4 output dims of one head
+// with an online merge (all loads of a round issued first, through
+// range-checked buffer resources: splits past nstate read as zero and get
+// weight 0); the 64 lanes then combine with xor shuffles.
 template <bool ROPE>
 __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
     const uint32_t lane = threadIdx.x;
@@ -309,9 +369,9 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
 #pragma unroll
         for (int u = 0; u < kMergeRound; ++u) {
             const uint32_t c = base + 64u * (uint32_t)u;
-            mc[u] = buf_ldf(rpm, c * 4u);
-            lc[u] = buf_ldf(rps, c * 4u);
-            ac[u] = buf_ldf4(rpo, c * (kD * 4u) + dbyte);
+            mc[u] = buf_ldf<0>(rpm, c * 4u);
+            lc[u] = buf_ldf<0>(rps, c * 4u);
+            ac[u] = buf_ldf4<0>(rpo, c * (kD * 4u) + dbyte);
         }
 #pragma unroll
         for (int u = 0; u < kMergeRound; ++u)
@@ -351,23 +411,16 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
         a.out[(uint64_t)h * kD + d0 + lane] = (f16)(v / den);
     }
     if constexpr (ROPE) {
-        // q rotated in place, as launch_rope_and_store_kv leaves it; every
-        // split workgroup has read it (the kernel boundary orders this)
-        if (a.apply && blockIdx.y < 8 && lane == 0) {
-            const uint32_t c8 = 8u * blockIdx.y;
-            f16* qh = a.q_rot + (uint64_t)h * kD;
-            f16x8 x0 = ld16(qh + c8), x1 = ld16(qh + 64 + c8);
-            rope_rotate8(x0, x1, ld16(a.cos_t + (uint64_t)a.row * (kD / 2) + c8),
-                         ld16(a.sin_t + (uint64_t)a.row * (kD / 2) + c8), x0, x1);
-            st16(qh + c8, x0);
-            st16(qh + 64 + c8, x1);
-        }
+        // every split workgroup has read q (the kernel boundary orders this)
+        if (a.apply && blockIdx.y < 8 && lane == 0) rotate_q_head(a, h, blockIdx.y);
     }
 }
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
+
+int decode_hpw(int path) { return path == 1 ? 4 : path == 2 ? 2 : path == 3 ? 1 : 0; }
 
 // path 1/2/3: 4/2/1 KV heads per workgroup
 const void* decode_split_symbol(int path, bool rope) {
@@ -388,21 +441,24 @@ const void* decode_merge_symbol(bool rope) {
                 : reinterpret_cast<const void*>(&flash_decode_merge<false>);
 }
 
+int decode_path_of_symbol(const void* fn, bool rope) {
+    for (int path = 1; path <= 3; ++path)
+        if (fn == decode_split_symbol(path, rope)) return path;
+    return 0;
+}
+
 DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_heads,
                        uint32_t head_dim, uint64_t kv_stride, const void* q, const void* k,
                        const void* v, int device) {
-    DecodePlan p{0, 1, kv_len, 1, 256};
+    DecodePlan p{0, 1, kv_len, 1, 256, 1};
     const uint32_t G = num_heads / num_kv_heads;
     const bool mfma_ok = head_dim == kD && G >= 1 && G <= 16 && kv_stride % 8 == 0 &&
                          kv_stride * 2 <= 0x40000000ull && aligned16(q) && aligned16(k) &&
                          aligned16(v) && get_option(kOptDecodeForceGeneric) == 0;
     if (!mfma_ok) return p;
-    // one KV head per workgroup up to kOneHeadMaxKeys keys (SmolLM3: 3-7 %
-    // faster than two from 64 to 8192 keys -- twice the workgroups on a
-    // context that does not fill the chip), two above when Hkv allows (3-8 %
-    // faster from 16384 keys: one head per workgroup streams slower and the
-    // merge reads twice the partial states; four heads per workgroup, which
-    // read whole 1 KiB cache rows, double the states again)
+    // one KV head per workgroup up to kOneHeadMaxKeys keys (SmolLM3: twice
+    // the workgroups on a context that does not fill the chip), two above
+    // when Hkv allows (fewer partial states to merge)
     uint32_t hpw = (num_kv_heads % 2 == 0 && kv_len > kOneHeadMaxKeys) ? 2 : 1;
     // a forced count is reduced to what Hkv allows
     const long hopt = get_option(kOptDecodeHeadsPerGroup);
@@ -412,7 +468,8 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
     }
     p.path = hpw == 4 ? 1 : hpw == 2 ? 2 : 3;
     p.block = 512;
-    const uint32_t groups = num_kv_heads / hpw;       // grid.y
+    const uint32_t groups = num_kv_heads / hpw;
+    p.groups = groups;
     // chunks are sized in steps of 8 keys (the waves mask the keys of a
     // partial batch): a step of one batch per wave (32 * 8/HPW keys) left up
     // to a third of the CUs idle just past multiples of 16384 keys (L = 32769:
@@ -446,14 +503,14 @@ DecodePlan replan_decode(DecodeArgs& a, int device) {
     return p;
 }
 
+dim3 decode_grid(const DecodeArgs& a, const DecodePlan& p) { return dim3(a.nsplit, p.groups); }
+
 hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,
                                bool rope) {
-    const int hpw = p.path == 1 ? 4 : p.path == 2 ? 2 : 1;
-    const dim3 grid(a.nsplit, a.num_kv_heads / hpw);
     if (p.path < 1 || p.path > 3) return hipErrorInvalidValue;
     const void* fn = decode_split_symbol(p.path, rope);
     void* args[1] = {const_cast<DecodeArgs*>(&a)};
-    return hipLaunchKernel(fn, grid, dim3(512), args, 0, stream);
+    return hipLaunchKernel(fn, decode_grid(a, p), dim3(512), args, 0, stream);
 }
 
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream, bool rope) {

@@ -266,6 +266,12 @@ def decode_plan(kv_len, num_heads, num_kv_heads, head_dim, kv_stride=0, q=None, 
             "nstate": out[4]}
 
 
+def decode_hpw(path: int) -> int:
+    """KV heads per split workgroup of a decode plan path: 4/2/1 for the MFMA
+    paths 1/2/3, 0 for the generic kernel."""
+    return {1: 4, 2: 2, 3: 1}.get(int(path), 0)
+
+
 def prefill_plan(q, k, v, out, num_heads, num_kv_heads, head_dim, q_stride=0, kv_stride=0):
     return int(lib().attn_prefill_plan(_ptr(q), _ptr(k), _ptr(v), _ptr(out), num_heads,
                                        num_kv_heads, head_dim, q_stride, kv_stride))

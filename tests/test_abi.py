@@ -133,6 +133,7 @@ def test_decode_plan_respects_workspace_capacity(attn):
                     # one KV head per workgroup up to 12288 keys
                     hpw = 2 if hkv % 2 == 0 and L > 12288 else 1
                     assert p["path"] == {4: 1, 2: 2, 1: 3}[hpw]
+                    assert attn.decode_hpw(p["path"]) == hpw
                     assert p["nsplit"] >= 1 and p["chunk"] * p["nsplit"] >= L
                     assert (p["nsplit"] - 1) * p["chunk"] < L  # no empty split
                     assert p["nstate"] == p["nsplit"]

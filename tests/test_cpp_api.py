@@ -137,3 +137,20 @@ def test_cpp_reference_api_program(gpu):
     lines = [l for l in r.stdout.splitlines() if l.startswith(("PASS", "FAIL"))]
     assert len(lines) == 9, r.stdout + r.stderr
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+def test_cpp_engine_order_first_decode_inside_global_capture(gpu):
+    """tests/cpp/test_engine_order.cpp in a process of its own: a prefill, then
+    the process's first decode call made inside a hipStreamCaptureModeGlobal
+    capture (model_inference.hpp:96-101), the graph launched, the next token
+    patched through the three updaters per layer and launched again; each token
+    equals eager launches bit for bit and an fp64 CPU attention."""
+    exe = ROOT / "tests" / "cpp" / "_build" / "test_engine_order"
+    assert exe.exists(), f"{exe} not built: run __graft_entry__.build()"
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    print(r.stdout)
+    print(r.stderr)
+    lines = [l for l in r.stdout.splitlines() if l.startswith(("PASS", "FAIL"))]
+    assert len(lines) == 6, r.stdout + r.stderr
+    assert r.returncode == 0, r.stdout + r.stderr

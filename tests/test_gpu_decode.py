@@ -140,7 +140,7 @@ def test_decode_heads_per_workgroup(attn, gpu, hpw):
     try:
         plan = attn.decode_plan(L, 16, 4, 128)
         print(f"[case] decode hpw={hpw} plan={plan}", flush=True)
-        assert plan["path"] == {4: 1, 2: 2, 1: 3}[hpw]
+        assert attn.decode_hpw(plan["path"]) == hpw
         got = run_decode(attn, gpu, q, k, v, L, 16, 4, 128)
     finally:
         attn.set_option("decode_heads_per_workgroup", 0)
@@ -258,10 +258,10 @@ def test_decode_graph_node_update_other_paths(attn, gpu, Hq, Hkv, hpw, L0):
     out_g = torch.empty(Hq * D, dtype=torch.float16, device=gpu)
     out_e = torch.empty(Hq * D, dtype=torch.float16, device=gpu)
     attn.set_option("decode_heads_per_workgroup", hpw)
-    for L, expect_path in ((Lmax, 1 if hpw == 4 else (2 if Hkv % 2 == 0 else 3)),
-                           (12288, 1 if hpw == 4 else 3), (12289, 1 if hpw == 4 else
-                                                           (2 if Hkv % 2 == 0 else 3))):
-        assert attn.decode_plan(L, Hq, Hkv, D)["path"] == expect_path, L
+    for L, expect_hpw in ((Lmax, 4 if hpw == 4 else (2 if Hkv % 2 == 0 else 1)),
+                          (12288, 4 if hpw == 4 else 1), (12289, 4 if hpw == 4 else
+                                                          (2 if Hkv % 2 == 0 else 1))):
+        assert attn.decode_hpw(attn.decode_plan(L, Hq, Hkv, D)["path"]) == expect_hpw, L
     stream = torch.cuda.Stream()
     sp = stream.cuda_stream
     anode, mnode = ctypes.c_void_p(), ctypes.c_void_p()
@@ -316,3 +316,30 @@ def test_decode_mfma_padded_kv_stride(attn, gpu):
     got = run_decode(attn, gpu, q, k, v, L, Hq, Hkv, D, kv_stride=kvs)
     _, e32 = oracle.attention(q, k, v, 1, Hq, Hkv, D, Hq * D, kvs, L, L - 1, causal=False)
     assert_close(got, e32.reshape(-1), 2e-3, 1e-2, "padded kv_stride")
+
+
+def test_decode_back_to_back_on_one_workspace(attn, gpu):
+    """Calls queued back to back on one stream and one workspace, alternating
+    inputs and lengths (so the partial states land at shifting places and
+    split counts), each give their own oracle result: no call reads another's
+    states."""
+    Hq, Hkv, D = 16, 4, 128
+    Ls = (32768, 5000, 32768, 777, 20001, 32768)
+    inputs = {L: smol_inputs(L, seed=30 + i) for i, L in enumerate(sorted(set(Ls)))}
+    dev_in = {L: tuple(dev(x, gpu) for x in inputs[L]) for L in inputs}
+    po, pm, ps = attn.decode_workspace(Hq, max(Ls), D, device=gpu)
+    outs = [torch.empty(Hq * D, dtype=torch.float16, device=gpu) for _ in range(3 * len(Ls))]
+    for rep in range(3):
+        for i, L in enumerate(Ls):
+            dq, dk, dv = dev_in[L]
+            attn.decode(dq, dk, dv, outs[rep * len(Ls) + i], po, pm, ps, 1, L, L - 1, Hq, Hkv, D,
+                        0, 0)
+    torch.cuda.synchronize()
+    exp = {L: expected(*inputs[L], L) for L in inputs}
+    for rep in range(3):
+        for i, L in enumerate(Ls):
+            print(f"[case] back-to-back rep={rep} L={L}", flush=True)
+            got = host(outs[rep * len(Ls) + i])
+            assert_close(got, exp[L], 2e-3, 1e-2, f"rep={rep} L={L}")
+            if rep:
+                assert np.array_equal(got, host(outs[i])), (rep, L)
