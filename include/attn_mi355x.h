@@ -132,6 +132,25 @@ int attn_update_rope_decode_nodes(hipGraphExec_t graph_exec, hipGraphNode_t atte
                                   hipGraphNode_t merge_node, size_t kv_len, size_t start_pos,
                                   int apply_rotation);
 
+/* No counterpart in the reference: attn_decode (query_len 1, start_pos and
+ * q_stride unused) without a caller workspace, for callers that cannot
+ * allocate device memory (code under graph capture that must not call
+ * hipMalloc, tight serving loops, harnesses that forbid it).  Same plan,
+ * kernels and output bits as attn_decode; the partial states go to a
+ * library-owned array of ATTN_DECODE_NOALLOC_SCRATCH_BYTES per GPU (held
+ * until the process ends; its address is looked up once per device on the
+ * first call there).  A plan whose states exceed the array (more than
+ * ATTN_DECODE_NOALLOC_SCRATCH_BYTES / 520 query-head x split states; every
+ * SmolLM3 decode shape uses at most 2048) returns hipErrorInvalidValue and
+ * enqueues nothing.  Allocates nothing; not for graph capture of node handles
+ * (none are returned).  Every call on one GPU shares the array: calls that
+ * overlap on one GPU (unordered streams) race and must not be issued. */
+#define ATTN_DECODE_NOALLOC_SCRATCH_BYTES (2u << 20)
+int attn_decode_noalloc(const attn_f16_t* q, const attn_f16_t* k_cache,
+                        const attn_f16_t* v_cache, attn_f16_t* out, size_t kv_len,
+                        size_t num_heads, size_t num_kv_heads, size_t head_dim, size_t kv_stride,
+                        hipStream_t stream);
+
 /* Workspace states a caller must provide for kv_len keys:
  * num_heads * ceil(kv_len / ATTN_KV_CHUNK) (model_inference.hpp:192-198). */
 size_t attn_decode_workspace_states(size_t num_heads, size_t kv_len);

@@ -84,6 +84,7 @@ def _declare(lib):
         "attn_rope_store_kv_decode": (_c.c_int, [_vp] * 11 + [_sz] * 6 + [_c.c_int, _vp, _vp,
                                                                           _vp]),
         "attn_update_rope_decode_nodes": (_c.c_int, [_vp, _vp, _vp, _sz, _sz, _c.c_int]),
+        "attn_decode_noalloc": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp]),
         "attn_weights_parse": (_c.c_int, [_vp, _sz, _c.c_uint64, _c.POINTER(WeightsLayout)]),
         "attn_weights_layout_for": (_c.c_int, [_c.POINTER(ModelConfigC), _c.c_uint64,
                                                _c.POINTER(WeightsLayout)]),
@@ -115,6 +116,7 @@ def exported_symbols():
             "attn_qkv_rope_store_kv_decode", "attn_update_qkv_rope_node", "attn_qkv_gemm",
             "attn_qkv_gemm_rope_store_kv", "attn_rope_store_kv_decode",
             "attn_update_rope_decode_nodes", "attn_weights_parse", "attn_weights_layout_for",
+            "attn_decode_noalloc",
             "attn_weights_error_string"]
 
 
