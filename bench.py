@@ -337,7 +337,12 @@ def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769, producer="rope"):
     as the decode's two kernels (attn_rope_store_kv_decode, 72 nodes).
     producer "qkv_fused" / "qkv_two" start each layer from a hidden vector
     instead: the QKV GEMV (2048 -> 3072, per-layer weights) fused with the
-    RoPE/append (108 nodes) or as the reference's two launches (144 nodes)."""
+    RoPE/append (108 nodes) or as the reference's two launches (144 nodes).
+    producer "o_proj_two" / "o_proj_fused" end each layer with the attention
+    output projection (per-layer W_o [2048][2048], beta = 1 into one residual
+    vector): the reference's launch after the merge (144 nodes) or the merge
+    fused into it (attn_decode_out_proj with decode_out_proj_fused = 1, 108
+    nodes)."""
     dev = torch.device("cuda:0")
     S = L
     cache = torch.empty(layers * 2 * S * KV_DIM, dtype=torch.float16, device=dev)
@@ -360,6 +365,10 @@ def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769, producer="rope"):
     if producer.startswith("qkv"):
         ws = rand16(torch, layers * QKV * HIDDEN, 600, 1.0 / 45)
         x = rand16(torch, HIDDEN, 599)
+    if producer.startswith("o_proj"):
+        wo = rand16(torch, layers * HIDDEN * Q_DIM, 700, 1.0 / 45)
+        y = rand16(torch, HIDDEN, 701)
+        ows = A.decode_out_proj_workspace(HQ, HIDDEN, device=dev)
 
     def enqueue():
         for l in range(layers):
@@ -388,15 +397,32 @@ def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769, producer="rope"):
                                                 vc, dcos.data_ptr(), dsin.data_ptr(), 1, HQ, HKV,
                                                 D, QKV, QKV, start_pos, apply, sp)
             assert rc == 0
+            if producer == "o_proj_fused":
+                rc = lib.attn_decode_out_proj(
+                    s, kc, vc, out[l].data_ptr(), po.data_ptr(), pm.data_ptr(), ps.data_ptr(), L,
+                    HQ, HKV, D, KV_DIM, wo.data_ptr() + 2 * l * HIDDEN * Q_DIM, y.data_ptr(),
+                    HIDDEN, 1.0, ows.data_ptr(), sp, None, None)
+                assert rc == 0
+                continue
             rc = lib.attn_decode(s, kc, vc, out[l].data_ptr(), po.data_ptr(), pm.data_ptr(),
                                  ps.data_ptr(), 1, L, start_pos, HQ, HKV, D, QKV, KV_DIM, sp,
                                  None, None)
             assert rc == 0
+            if producer == "o_proj_two":
+                rc = lib.attn_out_proj_decode(out[l].data_ptr(), y.data_ptr(),
+                                              wo.data_ptr() + 2 * l * HIDDEN * Q_DIM, HIDDEN, HQ,
+                                              D, 1.0, sp)
+                assert rc == 0
 
     with torch.cuda.stream(stream):
-        hipgraph.begin_capture(sp)
-        enqueue()
-        graph, exe = hipgraph.end_capture(sp)
+        if producer == "o_proj_fused":
+            A.set_option("decode_out_proj_fused", 1)
+        try:
+            hipgraph.begin_capture(sp)
+            enqueue()
+            graph, exe = hipgraph.end_capture(sp)
+        finally:
+            A.set_option("decode_out_proj_fused", 0)
         hipgraph.launch(exe, sp)
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
@@ -413,6 +439,9 @@ def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769, producer="rope"):
     if producer.startswith("qkv"):
         byts += layers * qkv_bytes()
         del ws
+    if producer.startswith("o_proj"):
+        byts += layers * 2 * HIDDEN * Q_DIM
+        del wo
     del cache
     return ms, byts
 
@@ -742,6 +771,12 @@ def main():
             p: {"us": v[0] * 1e3, "bytes": v[1], "GBps": v[1] / v[0] / 1e6} for p, v in c5q.items()}
         log(f"C5 with the QKV projection: fused producer {c5q['qkv_fused'][0] * 1e3:.1f} us, "
             f"GEMV + RoPE {c5q['qkv_two'][0] * 1e3:.1f} us")
+        c5o = {p: bench_c5(torch, A, hipgraph, 10, producer=p)
+               for p in ("o_proj_two", "o_proj_fused")}
+        detail["c5_with_out_projection"] = {
+            p: {"us": v[0] * 1e3, "bytes": v[1], "GBps": v[1] / v[0] / 1e6} for p, v in c5o.items()}
+        log(f"C5 with o_proj: split + merge + GEMV {c5o['o_proj_two'][0] * 1e3:.1f} us, "
+            f"split + merge fused into o_proj {c5o['o_proj_fused'][0] * 1e3:.1f} us")
 
     cpu = None
     if not args.no_cpu:

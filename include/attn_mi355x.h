@@ -185,6 +185,46 @@ int attn_qkv_rope_store_kv_decode(const attn_f16_t* x, attn_f16_t* y, const attn
 int attn_update_qkv_rope_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t start_pos,
                               int apply_rotation);
 
+/* launch_attention_out_projection_decode (kernels.hpp:179-187;
+ * attention_out_projection.hip.cpp:61-71, the GEMV of
+ * matrix_vec_mul.hip.cpp:79-172): y[hidden_size] = W[hidden_size][num_heads *
+ * head_dim] x + beta * y, fp16 in, fp32 accumulation (beta * y added to the
+ * fp32 sum when beta != 0), fp16 out.  hidden_size == 0 is a no-op; an empty
+ * row (num_heads * head_dim == 0) leaves beta * y.  The engine calls it with
+ * beta = 1 on the residual stream (model_inference.hpp:390-397). */
+int attn_out_proj_decode(const attn_f16_t* x, attn_f16_t* y, const attn_f16_t* w,
+                         size_t hidden_size, size_t num_heads, size_t head_dim, float beta,
+                         hipStream_t stream);
+
+/* No single counterpart in the reference: launch_causal_attention_decode(q,
+ * k_cache, v_cache, attn_out, partials, 1, kv_len, kv_len - 1, Hq, Hkv, D, 0,
+ * kv_stride, ...) followed by launch_attention_out_projection_decode(attn_out,
+ * y, w_o, hidden_size, Hq, D, beta) -- the pair ModelInference issues per layer
+ * in every decode step (model_inference.hpp:371-397).  By default it issues
+ * exactly those two launches (split + merge kernels, then the o_proj GEMV).
+ * With attn_set_option("decode_out_proj_fused", 1), decode shapes on the MFMA
+ * path (head_dim 128) run the split kernel (*attention_node) and one kernel
+ * that merges each head's partial states and multiplies the result by W_o
+ * (*merge_node); attn_out still receives the attention output, and y matches
+ * the pair within fp32 rounding of the partial sums (heads summed in order;
+ * deterministic).  The fused form is measured slower on MI355X (its cross-XCD
+ * reduction of the heads costs more than the kernel boundary it removes) and
+ * stays selectable for that measurement.  Other shapes, or a null workspace,
+ * always issue the two launches.  out_proj_workspace:
+ * attn_decode_out_proj_workspace_bytes(Hq, hidden_size) bytes, 256-byte
+ * aligned, ZERO-FILLED once before the first call; every call leaves its
+ * counters zero again.  Calls sharing a workspace must be ordered (one
+ * stream); update_merge/attn_update_merge_node patches the fused node like
+ * the merge node. */
+size_t attn_decode_out_proj_workspace_bytes(size_t num_heads, size_t hidden_size);
+int attn_decode_out_proj(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t* v_cache,
+                         attn_f16_t* attn_out, float* partial_out, float* partial_max,
+                         float* partial_sum, size_t kv_len, size_t num_heads,
+                         size_t num_kv_heads, size_t head_dim, size_t kv_stride,
+                         const attn_f16_t* w_o, attn_f16_t* y, size_t hidden_size, float beta,
+                         void* out_proj_workspace, hipStream_t stream,
+                         hipGraphNode_t* attention_node, hipGraphNode_t* merge_node);
+
 /* launch_qkv_gemm (kernels.hpp:29-36; qkv_gemm.hip.cpp:7-105, a rocBLAS
  * gemm_ex with fp32 compute): y[seq_len][total_qkv_dim] =
  * x[seq_len][hidden_size] . W[total_qkv_dim][hidden_size]^T, fp16 in, fp32

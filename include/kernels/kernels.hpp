@@ -151,6 +151,55 @@ void update_causal_attention_decode_node(
     size_t kv_cache_len
 );
 
+// kernels.hpp:179-187: y = W_o x + beta * y (beta = 1 adds the residual).
+void launch_attention_out_projection_decode(
+    const __half* d_in,               // [num_heads * head_dim]
+    __half* d_out,                    // [hidden_size]: residual in, projection out
+    const __half* d_o_proj_weights,   // [hidden_size][num_heads * head_dim]
+    size_t hidden_size,
+    size_t num_heads,
+    size_t head_dim,
+    float beta,
+    hipStream_t stream = nullptr
+);
+
+// Not in the reference: launch_causal_attention_decode_vectorized (query_len
+// 1, start_pos kv_cache_len - 1) followed by
+// launch_attention_out_projection_decode(d_attn_out, d_out, d_o_proj_weights,
+// hidden_size, num_heads, head_dim, beta) (model_inference.hpp:371-397), as
+// those launches; with the library option decode_out_proj_fused = 1 the
+// decode's merge and the projection run as one kernel (measured slower on
+// MI355X): *attention_node is the split kernel, *merge_node the merge (or
+// fused) kernel, both patched by the existing updaters.  d_attn_out receives
+// the attention output either way.  d_workspace:
+// decode_out_projection_workspace_bytes(num_heads, hidden_size) bytes,
+// zero-filled once before the first call (calls leave it reusable); calls
+// sharing it must be ordered on one stream.  Shapes off the fused path issue
+// the two launches.
+size_t decode_out_projection_workspace_bytes(size_t num_heads, size_t hidden_size);
+void launch_causal_attention_decode_out_projection(
+    const __half* d_q,
+    const __half* d_k_cache,
+    const __half* d_v_cache,
+    __half* d_attn_out,
+    float* d_partial_out,
+    float* d_partial_max,
+    float* d_partial_weight_sum,
+    size_t kv_cache_len,
+    size_t num_heads,
+    size_t num_kv_heads,
+    size_t head_dim,
+    size_t kv_stride,
+    const __half* d_o_proj_weights,
+    __half* d_out,
+    size_t hidden_size,
+    float beta,
+    void* d_workspace,
+    hipStream_t stream = nullptr,
+    hipGraphNode_t* attention_node = nullptr,
+    hipGraphNode_t* merge_node = nullptr
+);
+
 // Not in the reference: launch_qkv_decode followed by launch_rope_and_store_kv
 // for one decode token (model_inference.hpp:354-369), fused into one kernel
 // with identical results; d_qkv_out receives Q rotated, K and V as projected.

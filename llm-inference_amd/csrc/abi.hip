@@ -77,6 +77,7 @@ int attn_set_option(const char* name, long value) {
     else if (!std::strcmp(name, "qkv_gemm_tokens_per_wave")) which = kOptQkvGemmTokensPerWave;
     else if (!std::strcmp(name, "qkv_gemm_wide")) which = kOptQkvGemmWide;
     else if (!std::strcmp(name, "prefill_waves")) which = kOptPrefillWaves;
+    else if (!std::strcmp(name, "decode_out_proj_fused")) which = kOptDecodeOutProjFused;
     if (which < 0) return -1;
     g_options[which].store(value, std::memory_order_relaxed);
     return 0;
@@ -229,6 +230,22 @@ int attn_update_qkv_rope_node(hipGraphExec_t graph_exec, hipGraphNode_t node, si
     params.kernelParams = args;
     params.extra = nullptr;
     return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
+}
+
+int attn_out_proj_decode(const attn_f16_t* x, attn_f16_t* y, const attn_f16_t* w,
+                         size_t hidden_size, size_t num_heads, size_t head_dim, float beta,
+                         hipStream_t stream) {
+    if (hidden_size == 0) return 0;  // matrix_vec_mul.hip.cpp:160
+    const size_t in_dim = num_heads * head_dim;
+    if (!qkv_args_ok(x, y, w, in_dim, hidden_size)) return (int)hipErrorInvalidValue;
+    QkvArgs a{};
+    a.x = reinterpret_cast<const f16*>(x);
+    a.w = reinterpret_cast<const f16*>(w);
+    a.y = reinterpret_cast<f16*>(y);
+    a.out_dim = (uint32_t)hidden_size;
+    a.in_dim = (uint32_t)in_dim;
+    a.beta = beta;
+    return (int)launch_qkv_kernel(a, false, stream);
 }
 
 static int qkv_gemm_args(QkvGemmArgs& a, const attn_f16_t* x, attn_f16_t* y,
@@ -517,6 +534,88 @@ int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16
     return enqueue_decode(a, device, true, stream, attention_node, merge_node);
 }
 
+size_t attn_decode_out_proj_workspace_bytes(size_t num_heads, size_t hidden_size) {
+    return out_proj_workspace_bytes(num_heads, hidden_size);
+}
+
+int attn_decode_out_proj(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t* v_cache,
+                         attn_f16_t* attn_out, float* partial_out, float* partial_max,
+                         float* partial_sum, size_t kv_len, size_t num_heads,
+                         size_t num_kv_heads, size_t head_dim, size_t kv_stride,
+                         const attn_f16_t* w_o, attn_f16_t* y, size_t hidden_size, float beta,
+                         void* out_proj_workspace, hipStream_t stream,
+                         hipGraphNode_t* attention_node, hipGraphNode_t* merge_node) {
+    // the two launches this replaces, in the engine's order
+    // (model_inference.hpp:371-397), for every shape the fused kernel does
+    // not serve (their own no-op and error rules apply)
+    const auto two_launches = [&]() -> int {
+        int rc = attn_decode(q, k_cache, v_cache, attn_out, partial_out, partial_max,
+                             partial_sum, 1, kv_len, kv_len ? kv_len - 1 : 0, num_heads,
+                             num_kv_heads, head_dim, 0, kv_stride, stream, attention_node,
+                             merge_node);
+        if (rc != 0) return rc;
+        return attn_out_proj_decode(attn_out, y, w_o, hidden_size, num_heads, head_dim, beta,
+                                    stream);
+    };
+    // the two launches unless the fused kernel is asked for: on MI355X it is
+    // the slower form (its cross-XCD reduction of the heads costs more than
+    // the kernel boundary it removes)
+    if (get_option(kOptDecodeOutProjFused) != 1 || hidden_size == 0 || kv_len == 0 ||
+        num_kv_heads == 0 || head_dim == 0 || num_heads % num_kv_heads != 0 ||
+        !out_proj_workspace || !w_o || !y)
+        return two_launches();
+    if (!fits_u32(kv_len) || !fits_u32(num_heads) || !fits_u32(head_dim) ||
+        !fits_u32(hidden_size))
+        return (int)hipErrorInvalidValue;
+    if (!q || !k_cache || !v_cache || !attn_out || !partial_out || !partial_max || !partial_sum)
+        return (int)hipErrorInvalidValue;
+    const size_t kvs = kv_stride ? kv_stride : num_kv_heads * head_dim;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return (int)e;
+    OutProjArgs o{};
+    DecodeArgs& a = o.d;
+    a.q = reinterpret_cast<const f16*>(q);
+    a.k = reinterpret_cast<const f16*>(k_cache);
+    a.v = reinterpret_cast<const f16*>(v_cache);
+    a.out = reinterpret_cast<f16*>(attn_out);
+    a.part_out = partial_out;
+    a.part_max = partial_max;
+    a.part_sum = partial_sum;
+    a.kv_stride = kvs;
+    a.kv_len = (uint32_t)kv_len;
+    a.num_heads = (uint32_t)num_heads;
+    a.num_kv_heads = (uint32_t)num_kv_heads;
+    a.group = (uint32_t)(num_heads / num_kv_heads);
+    a.head_dim = (uint32_t)head_dim;
+    a.scale_log2 = scale_log2_for(head_dim);
+    o.w = reinterpret_cast<const f16*>(w_o);
+    o.y = reinterpret_cast<f16*>(y);
+    o.hidden = (uint32_t)hidden_size;
+    o.row_blocks = (uint32_t)((hidden_size + kOutProjRows - 1) / kOutProjRows);
+    o.beta = beta;
+    o.xcd_map = num_heads % 8 == 0 ? 1u : 0u;
+    const size_t part = out_proj_workspace_bytes(num_heads, hidden_size) -
+                        (size_t)o.row_blocks * sizeof(uint32_t);
+    o.y_part = static_cast<float*>(out_proj_workspace);
+    o.counters = reinterpret_cast<uint32_t*>(static_cast<char*>(out_proj_workspace) + part);
+    const DecodePlan p = replan_decode(a, device);
+    if (p.path < 1 || p.path > 3 || !out_proj_fused_ok(o)) return two_launches();
+    e = launch_decode_split(a, p, stream, false);
+    if (e != hipSuccess) return (int)e;
+    if (attention_node) {
+        e = captured_node(stream, attention_node);
+        if (e != hipSuccess) return (int)e;
+    }
+    e = launch_merge_out_proj(o, stream, false);
+    if (e != hipSuccess) return (int)e;
+    if (merge_node) {
+        e = captured_node(stream, merge_node);
+        if (e != hipSuccess) return (int)e;
+    }
+    return 0;
+}
+
 // Re-point a captured split node at kv_len: its kernel (heads per
 // workgroup), grid and arguments.
 static hipError_t replan_split_node(hipGraphExec_t graph_exec, hipGraphNode_t node,
@@ -586,11 +685,25 @@ static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, siz
         params.extra = nullptr;
         return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
     }
+    int device = 0;
+    if (params.func == merge_out_proj_symbol(false)) {
+        // the merge fused into o_proj: its decode arguments follow kv_len
+        if (!merge) return (int)hipErrorInvalidValue;
+        OutProjArgs o = *reinterpret_cast<const OutProjArgs*>(params.kernelParams[0]);
+        e = hipGetDevice(&device);
+        if (e != hipSuccess) return (int)e;
+        o.d.kv_len = (uint32_t)kv_len;
+        const DecodePlan p = replan_decode(o.d, device);
+        if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
+        void* args[1] = {&o};
+        params.kernelParams = args;
+        params.extra = nullptr;
+        return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
+    }
     const bool is_split = decode_path_of_symbol(params.func, false) != 0;
     const bool is_merge = params.func == decode_merge_symbol();
     if ((merge && !is_merge) || (!merge && !is_split)) return (int)hipErrorInvalidValue;
     DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(params.kernelParams[0]);
-    int device = 0;
     e = hipGetDevice(&device);
     if (e != hipSuccess) return (int)e;
     a.kv_len = (uint32_t)kv_len;

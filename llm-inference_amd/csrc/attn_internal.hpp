@@ -46,7 +46,7 @@ struct QkvArgs {
     uint32_t head_dim;
     uint32_t start_pos;  // fused: cache/table row (patched per decode step)
     uint32_t apply;      // fused: 1 rotate Q and K, 0 NoPE (patched)
-    uint32_t pad_;
+    float beta;          // unfused: y = W x + beta * y (the o_proj residual add); 0 for QKV
 };
 
 // Prefill QKV projection Y[M][N] = X[M][K] . W[N][K]^T (fp16 in, fp32
@@ -119,6 +119,20 @@ struct DecodeArgs {
     uint32_t apply;      // 1: rotate q and K; 0: copy K and V only (patched)
 };
 
+// q head h (D = 128) rotated in place by lanes 0..7 of the calling threads
+// (lane e: pairs 8e..8e+7 and their partners 64 + 8e..), as
+// launch_rope_and_store_kv leaves it; used by the merge kernels of the fused
+// RoPE + decode form once every split workgroup has read q.
+__device__ __forceinline__ void rotate_q_head(const DecodeArgs& a, uint32_t h, uint32_t e) {
+    const uint32_t c8 = 8u * e;
+    f16* qh = a.q_rot + (uint64_t)h * 128u;
+    f16x8 x0 = ld16(qh + c8), x1 = ld16(qh + 64 + c8);
+    rope_rotate8(x0, x1, ld16(a.cos_t + (uint64_t)a.row * 64u + c8),
+                 ld16(a.sin_t + (uint64_t)a.row * 64u + c8), x0, x1);
+    st16(qh + c8, x0);
+    st16(qh + 64 + c8, x1);
+}
+
 struct DecodePlan {
     // 0 = generic (any D, any stride); 1/2/3 = MFMA split kernel with 4/2/1 KV
     // heads per workgroup + merge kernel
@@ -148,6 +162,32 @@ hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream, bool rop
 const void* decode_split_symbol(int path, bool rope = false);
 const void* decode_merge_symbol(bool rope = false);
 int decode_path_of_symbol(const void* fn, bool rope);  // 0 when not a split kernel
+
+// Decode attention's partial-state merge fused into the attention output
+// projection (o_proj, y = W_o attn + beta y): workgroup (head h, row block)
+// merges head h's partial states into the head's fp16 attention output (the
+// merge kernel's result, written to d.out by row block 0) and multiplies it by
+// head h's columns of W_o for the block's rows; the fp32 products go to
+// y_part[h][row].  The last workgroup of a row block to finish (an atomic
+// count per block) sums the heads in order, adds beta * y and stores y in
+// fp16, then clears its count for the next call.
+struct OutProjArgs {
+    DecodeArgs d;          // the decode's arguments (states, plan; patched with kv_len)
+    const f16* w;          // W_o [hidden][num_heads * 128] row-major
+    f16* y;                // [hidden]: residual in (beta != 0), projection out
+    float* y_part;         // [num_heads][hidden] fp32 workspace
+    uint32_t* counters;    // [row_blocks], zero before the first call (left zero)
+    uint32_t hidden;
+    uint32_t row_blocks;   // ceil(hidden / 128)
+    float beta;
+    uint32_t xcd_map;      // 1: a head's workgroups share one XCD (num_heads % 8 == 0)
+};
+constexpr uint32_t kOutProjRows = 128;  // W_o rows per workgroup
+// workspace bytes: y_part, then the counters
+size_t out_proj_workspace_bytes(size_t num_heads, size_t hidden);
+bool out_proj_fused_ok(const OutProjArgs& a);
+hipError_t launch_merge_out_proj(const OutProjArgs& a, hipStream_t stream, bool rope);
+const void* merge_out_proj_symbol(bool rope);
 
 // ------------------------------------------------------------- prefill
 struct PrefillArgs {
@@ -201,7 +241,8 @@ enum Option {
     kOptQkvGemmTokensPerWave = 5, // 0 = automatic; 32, 64 or 128
     kOptQkvGemmWide = 6,          // 0 = automatic; 1 = never; 2 = whenever the shape allows
     kOptPrefillWaves = 7,         // 0 = automatic; 4 or 8 waves per prefill workgroup
-    kOptCount = 8
+    kOptDecodeOutProjFused = 8,   // 1: attn_decode_out_proj runs the fused merge + o_proj kernel
+    kOptCount = 9
 };
 long get_option(int which);
 

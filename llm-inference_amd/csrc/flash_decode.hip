@@ -81,19 +81,6 @@ __device__ __forceinline__ f32x4 buf_ldf4(BufRsrc r, uint32_t byte_off) {
 // from moving stores across
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// q head h rotated in place by lanes 0..7 of the calling threads (lane e:
-// pairs 8e..8e+7 and their partners 64 + 8e..), as launch_rope_and_store_kv
-// leaves it
-__device__ __forceinline__ void rotate_q_head(const DecodeArgs& a, uint32_t h, uint32_t e) {
-    const uint32_t c8 = 8u * e;
-    f16* qh = a.q_rot + (uint64_t)h * kD;
-    f16x8 x0 = ld16(qh + c8), x1 = ld16(qh + 64 + c8);
-    rope_rotate8(x0, x1, ld16(a.cos_t + (uint64_t)a.row * (kD / 2) + c8),
-                 ld16(a.sin_t + (uint64_t)a.row * (kD / 2) + c8), x0, x1);
-    st16(qh + c8, x0);
-    st16(qh + 64 + c8, x1);
-}
-
 // The split kernel: grid (nsplit, Hkv / HPW); workgroup (c, grp) owns chunk c
 // of KV heads HPW*grp .. HPW*grp + HPW-1.  Wave w serves KV head
 // HPW*grp + w % HPW and every (8/HPW)-th batch of the chunk, so the waves of a

@@ -73,6 +73,32 @@ void update_qkv_rope_and_store_kv_node(hipGraphExec_t graph_exec, hipGraphNode_t
                                                     apply_rotation ? 1 : 0));
 }
 
+void launch_attention_out_projection_decode(const __half* d_in, __half* d_out,
+                                            const __half* d_o_proj_weights, size_t hidden_size,
+                                            size_t num_heads, size_t head_dim, float beta,
+                                            hipStream_t stream) {
+    report(attn_out_proj_decode(h(d_in), h(d_out), h(d_o_proj_weights), hidden_size, num_heads,
+                                head_dim, beta, stream));
+}
+
+size_t decode_out_projection_workspace_bytes(size_t num_heads, size_t hidden_size) {
+    return attn_decode_out_proj_workspace_bytes(num_heads, hidden_size);
+}
+
+void launch_causal_attention_decode_out_projection(
+    const __half* d_q, const __half* d_k_cache, const __half* d_v_cache, __half* d_attn_out,
+    float* d_partial_out, float* d_partial_max, float* d_partial_weight_sum, size_t kv_cache_len,
+    size_t num_heads, size_t num_kv_heads, size_t head_dim, size_t kv_stride,
+    const __half* d_o_proj_weights, __half* d_out, size_t hidden_size, float beta,
+    void* d_workspace, hipStream_t stream, hipGraphNode_t* attention_node,
+    hipGraphNode_t* merge_node) {
+    report(attn_decode_out_proj(h(d_q), h(d_k_cache), h(d_v_cache), h(d_attn_out), d_partial_out,
+                                d_partial_max, d_partial_weight_sum, kv_cache_len, num_heads,
+                                num_kv_heads, head_dim, kv_stride, h(d_o_proj_weights),
+                                h(d_out), hidden_size, beta, d_workspace, stream,
+                                attention_node, merge_node));
+}
+
 void launch_rope(__half* d_q, __half* d_k, const __half* d_cos, const __half* d_sin,
                  size_t seq_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
                  size_t q_stride, size_t k_stride, size_t start_pos) {

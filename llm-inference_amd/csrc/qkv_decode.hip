@@ -2,7 +2,10 @@
 // append of the same step folded into its epilogue.
 //
 // Reference semantics: launch_qkv_decode (qkv_gemm.hip.cpp:107-116) is the
-// GEMV y = W x of matrix_vec_mul.hip.cpp:79-172 with beta = 0: W row-major
+// GEMV y = W x of matrix_vec_mul.hip.cpp:79-172 with beta = 0 (the unfused
+// kernel also serves launch_attention_out_projection_decode,
+// attention_out_projection.hip.cpp:61-71: the same GEMV with y += beta * y,
+// beta = 1 for the residual add): W row-major
 // [out_dim][in_dim] (the Q rows of all heads, then K, then V), x [in_dim],
 // fp32 accumulation, y rounded to fp16.  In a decode step the engine then runs
 // launch_rope_and_store_kv on y (model_inference.hpp:354-369): Q heads rotated
@@ -86,13 +89,18 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void qkv_gemv(QkvArgs a) {
         acc1 += xor_lane(acc1, o);
     }
     if (lane != 0) return;
-    const f16 y0 = (f16)acc0;
-    const f16 y1 = (f16)acc1;
     if (!FUSED) {
-        a.y[row0] = y0;
-        if (has_row1) a.y[row1] = y1;
+        // matrix_vec_mul.hip.cpp:156-163: the fp32 sum plus beta * y, rounded once
+        if (a.beta != 0.f) {
+            acc0 += a.beta * (float)a.y[row0];
+            if (has_row1) acc1 += a.beta * (float)a.y[row1];
+        }
+        a.y[row0] = (f16)acc0;
+        if (has_row1) a.y[row1] = (f16)acc1;
         return;
     }
+    const f16 y0 = (f16)acc0;
+    const f16 y1 = (f16)acc1;
     // fused RoPE + KV append on the fp16 GEMV outputs
     f16 r0 = y0, r1 = y1;
     if (a.apply) {

@@ -85,6 +85,10 @@ def _declare(lib):
                                                                           _vp]),
         "attn_update_rope_decode_nodes": (_c.c_int, [_vp, _vp, _vp, _sz, _sz, _c.c_int]),
         "attn_decode_noalloc": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp]),
+        "attn_out_proj_decode": (_c.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _c.c_float, _vp]),
+        "attn_decode_out_proj_workspace_bytes": (_sz, [_sz, _sz]),
+        "attn_decode_out_proj": (_c.c_int, [_vp] * 7 + [_sz] * 5 + [_vp, _vp, _sz, _c.c_float,
+                                                                    _vp, _vp, _vp, _vp]),
         "attn_weights_parse": (_c.c_int, [_vp, _sz, _c.c_uint64, _c.POINTER(WeightsLayout)]),
         "attn_weights_layout_for": (_c.c_int, [_c.POINTER(ModelConfigC), _c.c_uint64,
                                                _c.POINTER(WeightsLayout)]),
@@ -116,7 +120,8 @@ def exported_symbols():
             "attn_qkv_rope_store_kv_decode", "attn_update_qkv_rope_node", "attn_qkv_gemm",
             "attn_qkv_gemm_rope_store_kv", "attn_rope_store_kv_decode",
             "attn_update_rope_decode_nodes", "attn_weights_parse", "attn_weights_layout_for",
-            "attn_decode_noalloc",
+            "attn_decode_noalloc", "attn_out_proj_decode",
+            "attn_decode_out_proj_workspace_bytes", "attn_decode_out_proj",
             "attn_weights_error_string"]
 
 
@@ -256,6 +261,40 @@ def update_rope_decode_nodes(graph_exec, attention_node, merge_node, kv_len, sta
     rc = lib().attn_update_rope_decode_nodes(graph_exec, attention_node, merge_node, kv_len,
                                              start_pos, 1 if apply_rotation else 0)
     _check(rc, "attn_update_rope_decode_nodes")
+
+
+def out_proj_decode(x, y, w, hidden_size, num_heads, head_dim, beta, stream=None):
+    """launch_attention_out_projection_decode (kernels.hpp:179-187):
+    y = W x + beta y, fp16 out."""
+    rc = lib().attn_out_proj_decode(_ptr(x), _ptr(y), _ptr(w), hidden_size, num_heads,
+                                    head_dim, float(beta), _stream(stream))
+    _check(rc, "attn_out_proj_decode")
+
+
+def decode_out_proj_workspace(num_heads: int, hidden_size: int, device="cuda"):
+    """The zero-filled workspace attn_decode_out_proj needs (fp32 head partials
+    and per-row-block counters; every call leaves the counters zero)."""
+    n = int(lib().attn_decode_out_proj_workspace_bytes(num_heads, hidden_size))
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def decode_out_proj(q, k_cache, v_cache, attn_out, partial_out, partial_max, partial_sum,
+                    kv_len, num_heads, num_kv_heads, head_dim, w_o, y, hidden_size, beta,
+                    workspace, kv_stride=0, stream=None, nodes=None):
+    """launch_causal_attention_decode + launch_attention_out_projection_decode
+    of one decode step with the merge and the projection in one kernel (no
+    reference counterpart).  `nodes`, a list, receives the (split, merge)
+    graph nodes when capturing."""
+    an, mn = ctypes.c_void_p(), ctypes.c_void_p()
+    rc = lib().attn_decode_out_proj(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(attn_out), _ptr(partial_out),
+        _ptr(partial_max), _ptr(partial_sum), kv_len, num_heads, num_kv_heads, head_dim,
+        kv_stride, _ptr(w_o), _ptr(y), hidden_size, float(beta), _ptr(workspace),
+        _stream(stream), ctypes.byref(an) if nodes is not None else None,
+        ctypes.byref(mn) if nodes is not None else None)
+    _check(rc, "attn_decode_out_proj")
+    if nodes is not None:
+        nodes[:] = [an.value, mn.value]
 
 
 def decode_plan(kv_len, num_heads, num_kv_heads, head_dim, kv_stride=0, q=None, k=None,

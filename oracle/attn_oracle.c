@@ -39,6 +39,12 @@
  *                                     exactly; the reference's own
  *                                     test_matrix_vec_mul.cpp inputs (closed
  *                                     form) within its tolerance of fp64.
+ *   orc_gemv_beta                     beta = 0 equals orc_gemv bit for bit;
+ *                                     W = 0 leaves y (beta = 1) / gives
+ *                                     fp16(beta y); a hand-worked case whose
+ *                                     result differs when the product is
+ *                                     rounded to fp16 before the residual is
+ *                                     added (a double rounding fails).
  */
 #include <math.h>
 #include <stddef.h>
@@ -387,6 +393,28 @@ void orc_gemv(const uint16_t* w, const uint16_t* x, uint16_t* y, size_t out_dim,
         for (size_t c = 0; c < in_dim; ++c)
             acc += (double)orc_f16_to_f32(row[c]) * (double)orc_f16_to_f32(x[c]);
         y[r] = orc_f32_to_f16((float)acc);
+    }
+}
+
+/* y = W x + beta * y, the residual form of the same GEMV
+ * (matrix_vec_mul.hip.cpp:156-163; launch_attention_out_projection_decode,
+ * attention_out_projection.hip.cpp:61-71, with beta = 1 on the engine's
+ * residual stream, model_inference.hpp:390-397): the fp32 sum of W x (fp64
+ * here, rounded to fp32 as orc_gemv does), plus the fp32 product beta * y[r]
+ * when beta != 0, rounded once to fp16.  y is read and written in place. */
+void orc_gemv_beta(const uint16_t* w, const uint16_t* x, uint16_t* y, size_t out_dim,
+                   size_t in_dim, float beta) {
+    for (size_t r = 0; r < out_dim; ++r) {
+        const uint16_t* row = w + r * in_dim;
+        double acc = 0.0;
+        for (size_t c = 0; c < in_dim; ++c)
+            acc += (double)orc_f16_to_f32(row[c]) * (double)orc_f16_to_f32(x[c]);
+        float sum = (float)acc;
+        if (beta != 0.0f) {
+            const float res = beta * orc_f16_to_f32(y[r]);
+            sum = sum + res;
+        }
+        y[r] = orc_f32_to_f16(sum);
     }
 }
 

@@ -52,6 +52,7 @@ def lib():
         L.orc_kat_inputs.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, _sz]
         L.orc_gemv.argtypes = [_vp, _vp, _vp, _sz, _sz]
         L.orc_gemm.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz]
+        L.orc_gemv_beta.argtypes = [_vp, _vp, _vp, _sz, _sz, ctypes.c_float]
         _lib = L
     return _lib
 
@@ -145,6 +146,19 @@ def gemv(w, x):
     y = np.empty(out_dim, dtype=np.uint16)
     lib().orc_gemv(_p(w), _p(x), _p(y), out_dim, in_dim)
     return y
+
+
+def gemv_beta(w, x, y, beta):
+    """fp16(W x + beta y) with an fp64 sum rounded to fp32, then the fp32
+    residual add (attn_oracle.c:orc_gemv_beta); returns the new y."""
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    out_dim, in_dim = w.shape
+    assert x.shape == (in_dim,)
+    out = np.array(y, dtype=np.uint16, copy=True)
+    assert out.shape == (out_dim,)
+    lib().orc_gemv_beta(_p(w), _p(x), _p(out), out_dim, in_dim, float(beta))
+    return out
 
 
 def gemm(x, w):

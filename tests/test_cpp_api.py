@@ -58,6 +58,14 @@ EXPECTED = {
     "hipGraphNode**)",
     "update_rope_and_store_kv_decode_nodes(hipGraphExec*, hipGraphNode*, hipGraphNode*, "
     "unsigned long, unsigned long, bool)",
+    # kernels.hpp:179-187 of the reference, the decode step's consumer
+    "launch_attention_out_projection_decode(__half const*, __half*, __half const*, "
+    "unsigned long, unsigned long, unsigned long, float, ihipStream_t*)",
+    # decode with its merge fused into o_proj (no reference counterpart)
+    "launch_causal_attention_decode_out_projection(__half const*, __half const*, __half const*, "
+    "__half*, float*, float*, float*, unsigned long, unsigned long, unsigned long, unsigned long, "
+    "unsigned long, __half const*, __half*, unsigned long, float, void*, ihipStream_t*, "
+    "hipGraphNode**, hipGraphNode**)",
 }
 
 
@@ -83,6 +91,7 @@ def test_library_defines_every_reference_launcher(attn):
     exported = _exported_cpp_functions()
     missing = sorted(EXPECTED - exported)
     assert not missing, missing
+    assert "decode_out_projection_workspace_bytes(unsigned long, unsigned long)" in exported
 
 
 @pytest.mark.parametrize("std", ["c++17", "c++23"])

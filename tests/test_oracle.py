@@ -316,6 +316,42 @@ def test_gemv_reference_known_answers(out_dim, in_dim):
     assert np.all(np.abs(y - exp) <= 1e-3 + 1e-3 * np.abs(exp))
 
 
+def test_gemv_beta_zero_is_gemv_and_zero_weights_keep_residual():
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((70, 300)) / 17).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal(300).astype(np.float16).view(np.uint16)
+    y = rng.standard_normal(70).astype(np.float16).view(np.uint16)
+    # beta = 0 ignores y (NaN included: it is never read)
+    nan = np.full(70, np.float16(np.nan).view(np.uint16), np.uint16)
+    assert np.array_equal(oracle.gemv_beta(w, x, nan, 0.0), oracle.gemv(w, x))
+    # W = 0: the residual alone, y itself for beta = 1, fp16(beta y) otherwise
+    zero = np.zeros_like(w)
+    assert np.array_equal(oracle.gemv_beta(zero, x, y, 1.0), y)
+    exp = (np.float32(0.75) * f16(y).astype(np.float32)).astype(np.float16)
+    assert np.array_equal(oracle.gemv_beta(zero, x, y, 0.75), exp.view(np.uint16))
+    # against numpy float64 + the residual, rounded once (one fp16 ulp at most)
+    ref = ((w.view(np.float16).astype(np.float64) @ x.view(np.float16).astype(np.float64))
+           + f16(y).astype(np.float64)).astype(np.float16)
+    assert ulp_diff(oracle.gemv_beta(w, x, y, 1.0), ref.view(np.uint16)).max() <= 1
+
+
+def test_gemv_beta_rounds_once():
+    # W x = 1 + 2^-11 (exact in fp32, a tie in fp16 that rounds to 1) and
+    # y = 2^-12: the sum 1 + 3 * 2^-12 rounds once to 1 + 2^-10; rounding the
+    # product to fp16 first would give 1 + 2^-12 -> 1
+    w = np.array([[1.0, 2.0 ** -11]], np.float16).view(np.uint16)
+    x = np.array([1.0, 1.0], np.float16).view(np.uint16)
+    y = np.array([2.0 ** -12], np.float16).view(np.uint16)
+    assert f16(oracle.gemv_beta(w, x, y, 1.0))[0] == np.float16(1 + 2.0 ** -10)
+    assert f16(oracle.gemv(w, x))[0] == np.float16(1.0)
+    # a small hand-worked case: [1 2] . [3 4] + 0.5 = 11.5
+    w = np.array([[1.0, 2.0]], np.float16).view(np.uint16)
+    x = np.array([3.0, 4.0], np.float16).view(np.uint16)
+    y = np.array([0.5], np.float16).view(np.uint16)
+    assert f16(oracle.gemv_beta(w, x, y, 1.0))[0] == np.float16(11.5)
+    assert f16(oracle.gemv_beta(w, x, y, -2.0))[0] == np.float16(10.0)
+
+
 def test_gemm_rows_match_gemv_and_numpy():
     # orc_gemm is orc_gemv per token row; against numpy float64 on a
     # non-square product (a transposed operand has the wrong shape)
