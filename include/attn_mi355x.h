@@ -111,8 +111,10 @@ int attn_update_merge_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_
  * before reading it, the merge kernel leaves q rotated in place.  q, the
  * cache and out equal that pair's bit for bit.  Serves the MFMA decode path
  * (head_dim 128, 16-byte aligned tensors) with kv_stride = Hkv*D (or 0) and
- * start_pos < kv_len; other arguments return hipErrorInvalidValue and enqueue
- * nothing (issue attn_rope_store_kv and attn_decode instead).  The node
+ * start_pos < kv_len.  Other shapes called without node handles issue the
+ * pair itself (attn_rope_store_kv, then attn_decode); with node handles
+ * requested they return hipErrorInvalidValue and enqueue nothing, since
+ * attn_update_rope_decode_nodes patches only the fused pair.  The node
  * handles are the split and merge kernels, patched together by
  * attn_update_rope_decode_nodes. */
 int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16_t* v,

@@ -233,9 +233,11 @@ void update_qkv_rope_and_store_kv_node(
 // followed by launch_causal_attention_decode (model_inference.hpp:96-126) as
 // the decode's two kernels (split, merge) with identical results: q is left
 // rotated in place, the new K/V row appended at start_pos, d_out holds the
-// attention.  head_dim 128, 16-byte aligned tensors, cache rows
-// num_kv_heads * head_dim apart and start_pos < kv_cache_len; other arguments
-// are reported like a failed launch and nothing is enqueued.
+// attention.  Serves head_dim 128, 16-byte aligned tensors and start_pos <
+// kv_cache_len; other shapes issue the two reference launches when no node
+// handles are requested, and throw std::runtime_error (nothing enqueued) when
+// they are, since update_rope_and_store_kv_decode_nodes patches only the
+// fused pair.
 void launch_rope_and_store_kv_decode(
     __half* d_q,
     const __half* d_k,

@@ -494,10 +494,7 @@ int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16
     const size_t kvs = kv_stride ? kv_stride : kv_dim;
     // the fused kernels serve the MFMA decode path with the engine's cache
     // layout (RoPE writes rows kv_dim apart, rope.hip.cpp:110) and the new
-    // token inside the decoded range; other shapes are rejected
-    // (hipErrorInvalidValue, nothing enqueued): a caller issues
-    // attn_rope_store_kv and attn_decode for them
-    if (kvs != kv_dim || start_pos >= kv_len) return (int)hipErrorInvalidValue;
+    // token inside the decoded range
     const bool al = ((uintptr_t)k | (uintptr_t)v | (uintptr_t)cos_table | (uintptr_t)sin_table |
                      (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0;
     int device = 0;
@@ -506,7 +503,20 @@ int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16
     const DecodePlan p = plan_decode((uint32_t)kv_len, (uint32_t)num_heads,
                                      (uint32_t)num_kv_heads, (uint32_t)head_dim, kvs, q,
                                      k_cache, v_cache, device);
-    if (p.path == 0 || !al) return (int)hipErrorInvalidValue;
+    if (p.path == 0 || !al || kvs != kv_dim || start_pos >= kv_len) {
+        // Other shapes: eager calls issue the two launches this replaces;
+        // a capture asking for node handles is rejected (hipErrorInvalidValue,
+        // nothing enqueued), because attn_update_rope_decode_nodes could not
+        // patch that sequence as one pair
+        if (attention_node || merge_node) return (int)hipErrorInvalidValue;
+        const int rc = attn_rope_store_kv(q, const_cast<attn_f16_t*>(k), v, k_cache, v_cache,
+                                          cos_table, sin_table, 1, num_heads, num_kv_heads,
+                                          head_dim, 0, 0, start_pos, apply_rotation, stream);
+        if (rc != 0) return rc;
+        return attn_decode(q, k_cache, v_cache, out, partial_out, partial_max, partial_sum, 1,
+                           kv_len, start_pos, num_heads, num_kv_heads, head_dim, 0, kv_stride,
+                           stream, nullptr, nullptr);
+    }
     DecodeArgs a{};
     a.q = reinterpret_cast<const f16*>(q);
     a.k = reinterpret_cast<const f16*>(k_cache);

@@ -1,28 +1,31 @@
 // Definitions of the reference's attention launch API (include/kernels/kernels.hpp)
 // over the C ABI (include/attn_mi355x.h).  Behaviour follows the reference
-// launchers: they return void, silently skip the shapes the reference skips
-// (the C ABI returns 0 for those), leave errors for hipGetLastError()-style
-// checks by the caller, and the graph-node updaters exit through HIP_CHECK on
-// failure (causal_attention.hip.cpp:975-1026, rope.hip.cpp:208-241).
+// launchers: they return void and silently skip the shapes the reference skips
+// (the C ABI returns 0 for those); a call the library rejects (arguments it
+// cannot serve, or a failed kernel launch) throws std::runtime_error naming
+// the launcher and the HIP error, so nothing fails silently.  The graph-node
+// updaters exit through HIP_CHECK on failure, as the reference's do
+// (causal_attention.hip.cpp:975-1026, rope.hip.cpp:208-241).
 #include "../../include/kernels/kernels.hpp"
 
 #include "../../include/attn_mi355x.h"
 #include "../../include/gpu_utils.hpp"
+
+#include <stdexcept>
+#include <string>
 
 namespace {
 
 inline attn_f16_t* h(__half* p) { return reinterpret_cast<attn_f16_t*>(p); }
 inline const attn_f16_t* h(const __half* p) { return reinterpret_cast<const attn_f16_t*>(p); }
 
-// A failed launch is reported the way a failed <<<>>> launch is: through the
-// HIP runtime's last-error state, which callers check with hipGetLastError().
-inline void report(int rc) {
-    if (rc != 0) {
-        // nothing else to do: the launch helpers already left the runtime's
-        // error state set (hipGetLastError) when a kernel launch failed;
-        // argument errors are reported on stderr so they are not silent
-        std::fprintf(stderr, "[attn_mi355x] launch rejected: hipError %d\n", rc);
-    }
+// A non-zero C-ABI result: the launcher rejected its arguments or a kernel
+// launch failed (the HIP runtime's last-error state is also set then).
+inline void report(int rc, const char* launcher) {
+    if (rc != 0)
+        throw std::runtime_error(std::string("attn_mi355x: ") + launcher + " failed: " +
+                                 hipGetErrorString((hipError_t)rc) + " (" +
+                                 std::to_string(rc) + ")");
 }
 
 }  // namespace
@@ -31,7 +34,7 @@ void launch_qkv_gemm(const __half* d_input_norm, __half* d_qkv_out,
                      const __half* d_qkv_weights, const size_t seq_len,
                      const size_t hidden_size, const size_t total_qkv_dim) {
     report(attn_qkv_gemm(h(d_input_norm), h(d_qkv_out), h(d_qkv_weights), seq_len, hidden_size,
-                         total_qkv_dim, nullptr));
+                         total_qkv_dim, nullptr), "launch_qkv_gemm");
 }
 
 void launch_qkv_gemm_rope_and_store_kv(const __half* d_input_norm, __half* d_qkv_out,
@@ -44,14 +47,15 @@ void launch_qkv_gemm_rope_and_store_kv(const __half* d_input_norm, __half* d_qkv
     report(attn_qkv_gemm_rope_store_kv(h(d_input_norm), h(d_qkv_out), h(d_qkv_weights),
                                        h(d_k_cache), h(d_v_cache), h(d_cos), h(d_sin), seq_len,
                                        hidden_size, num_heads, num_kv_heads, head_dim, start_pos,
-                                       apply_rotation ? 1 : 0, stream));
+                                       apply_rotation ? 1 : 0, stream),
+           "launch_qkv_gemm_rope_and_store_kv");
 }
 
 void launch_qkv_decode(const __half* d_input_norm, __half* d_qkv_out,
                        const __half* d_qkv_weights, const size_t hidden_size,
                        const size_t total_qkv_dim, hipStream_t stream) {
     report(attn_qkv_decode(h(d_input_norm), h(d_qkv_out), h(d_qkv_weights), hidden_size,
-                           total_qkv_dim, stream));
+                           total_qkv_dim, stream), "launch_qkv_decode");
 }
 
 void launch_qkv_rope_and_store_kv_decode(const __half* d_input_norm, __half* d_qkv_out,
@@ -64,7 +68,8 @@ void launch_qkv_rope_and_store_kv_decode(const __half* d_input_norm, __half* d_q
     report(attn_qkv_rope_store_kv_decode(h(d_input_norm), h(d_qkv_out), h(d_qkv_weights),
                                          h(d_k_cache), h(d_v_cache), h(d_cos), h(d_sin),
                                          hidden_size, num_heads, num_kv_heads, head_dim,
-                                         start_pos, apply_rotation ? 1 : 0, stream));
+                                         start_pos, apply_rotation ? 1 : 0, stream),
+           "launch_qkv_rope_and_store_kv_decode");
 }
 
 void update_qkv_rope_and_store_kv_node(hipGraphExec_t graph_exec, hipGraphNode_t node,
@@ -78,7 +83,7 @@ void launch_attention_out_projection_decode(const __half* d_in, __half* d_out,
                                             size_t num_heads, size_t head_dim, float beta,
                                             hipStream_t stream) {
     report(attn_out_proj_decode(h(d_in), h(d_out), h(d_o_proj_weights), hidden_size, num_heads,
-                                head_dim, beta, stream));
+                                head_dim, beta, stream), "launch_attention_out_projection_decode");
 }
 
 size_t decode_out_projection_workspace_bytes(size_t num_heads, size_t hidden_size) {
@@ -92,18 +97,19 @@ void launch_causal_attention_decode_out_projection(
     const __half* d_o_proj_weights, __half* d_out, size_t hidden_size, float beta,
     void* d_workspace, hipStream_t stream, hipGraphNode_t* attention_node,
     hipGraphNode_t* merge_node) {
-    report(attn_decode_out_proj(h(d_q), h(d_k_cache), h(d_v_cache), h(d_attn_out), d_partial_out,
-                                d_partial_max, d_partial_weight_sum, kv_cache_len, num_heads,
-                                num_kv_heads, head_dim, kv_stride, h(d_o_proj_weights),
-                                h(d_out), hidden_size, beta, d_workspace, stream,
-                                attention_node, merge_node));
+    const int rc = attn_decode_out_proj(
+        h(d_q), h(d_k_cache), h(d_v_cache), h(d_attn_out), d_partial_out, d_partial_max,
+        d_partial_weight_sum, kv_cache_len, num_heads, num_kv_heads, head_dim, kv_stride,
+        h(d_o_proj_weights), h(d_out), hidden_size, beta, d_workspace, stream, attention_node,
+        merge_node);
+    report(rc, "launch_causal_attention_decode_out_projection");
 }
 
 void launch_rope(__half* d_q, __half* d_k, const __half* d_cos, const __half* d_sin,
                  size_t seq_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
                  size_t q_stride, size_t k_stride, size_t start_pos) {
     report(attn_rope(h(d_q), h(d_k), h(d_cos), h(d_sin), seq_len, num_heads, num_kv_heads,
-                     head_dim, q_stride, k_stride, start_pos, nullptr));
+                     head_dim, q_stride, k_stride, start_pos, nullptr), "launch_rope");
 }
 
 void launch_rope_and_store_kv(__half* d_q, __half* d_k, __half* d_v, __half* d_k_cache,
@@ -113,7 +119,8 @@ void launch_rope_and_store_kv(__half* d_q, __half* d_k, __half* d_v, __half* d_k
                               size_t start_pos, bool apply_rotation, hipStream_t stream) {
     report(attn_rope_store_kv(h(d_q), h(d_k), h(d_v), h(d_k_cache), h(d_v_cache), h(d_cos),
                               h(d_sin), seq_len, num_heads, num_kv_heads, head_dim, q_stride,
-                              k_stride, start_pos, apply_rotation ? 1 : 0, stream));
+                              k_stride, start_pos, apply_rotation ? 1 : 0, stream),
+           "launch_rope_and_store_kv");
 }
 
 void update_rope_and_store_kv_node(hipGraphExec_t graph_exec, hipGraphNode_t node,
@@ -127,7 +134,7 @@ void launch_causal_attention_prefill(const __half* d_q, const __half* d_k, const
                                      size_t num_kv_heads, size_t head_dim, size_t q_stride,
                                      size_t kv_stride) {
     report(attn_prefill(h(d_q), h(d_k), h(d_v), h(d_out), seq_len, num_heads, num_kv_heads,
-                        head_dim, q_stride, kv_stride, nullptr));
+                        head_dim, q_stride, kv_stride, nullptr), "launch_causal_attention_prefill");
 }
 
 void launch_causal_attention_decode(const __half* d_q, const __half* d_k_cache,
@@ -144,7 +151,7 @@ void launch_causal_attention_decode(const __half* d_q, const __half* d_k_cache,
     // gpu_utils.hpp:45-59: a capture that does not end in exactly one node throws
     if (rc == (int)hipErrorIllegalState && (attention_node || merge_node))
         throw std::runtime_error("Expected one capture dependency");
-    report(rc);
+    report(rc, "launch_causal_attention_decode");
 }
 
 void launch_causal_attention_decode_vectorized(
@@ -175,7 +182,7 @@ void launch_rope_and_store_kv_decode(__half* d_q, const __half* d_k, const __hal
     // gpu_utils.hpp:45-59: a capture that does not end in exactly one node throws
     if (rc == (int)hipErrorIllegalState && (attention_node || merge_node))
         throw std::runtime_error("Expected one capture dependency");
-    report(rc);
+    report(rc, "launch_rope_and_store_kv_decode");
 }
 
 void update_rope_and_store_kv_decode_nodes(hipGraphExec_t graph_exec,

@@ -20,6 +20,9 @@
 //      eager launch_rope_and_store_kv + decode, bit for bit.
 //   8. launch_qkv_gemm against an fp64 CPU product, and the fused
 //      launch_qkv_gemm_rope_and_store_kv against the two launches, bit for bit.
+//   9. launch_rope_and_store_kv_decode on a shape its fused kernels do not
+//      serve (start_pos == kv_cache_len): with node handles it throws and
+//      enqueues nothing; without, it equals the two reference launches.
 // Prints one PASS/FAIL line per test; exit status is the number of failures.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -29,6 +32,7 @@
 #include <cstdio>
 #include <cstring>
 #include <random>
+#include <stdexcept>
 #include <vector>
 
 #include "../../include/gpu_utils.hpp"
@@ -733,6 +737,80 @@ void test_qkv_gemm_prefill() {
     for (void* p : {(void*)dx, (void*)dw, (void*)y1, (void*)y2}) HIP_CHECK(hipFree(p));
 }
 
+// ---------------------------------------------------------------- test 9
+void test_fused_rope_decode_other_shape() {
+    const size_t heads = 8, kv_heads = 2, head_dim = 128, L = 40, start_pos = L;
+    const size_t q_dim = heads * head_dim, kv_dim = kv_heads * head_dim;
+    Config cfg{1, L + 4, kv_heads, head_dim};
+    KVCache fused_cache(cfg), two_cache(cfg);
+    RopeCache rope = create_rope_cache(cfg.max_seq_len, head_dim, 5.0e6f);
+    std::mt19937 gen(9);
+    std::normal_distribution<float> nd;
+    std::vector<__half> cache_init(2 * cfg.max_seq_len * kv_dim), qkv(q_dim + 2 * kv_dim);
+    for (auto& v : cache_init) v = __float2half(nd(gen));
+    for (auto& v : qkv) v = __float2half(nd(gen));
+    for (KVCache* c : {&fused_cache, &two_cache})
+        HIP_CHECK(hipMemcpy(c->get_k_cache(0), cache_init.data(), cache_init.size() * 2,
+                            hipMemcpyHostToDevice));
+    __half* a_f = upload(qkv);
+    __half* a_t = upload(qkv);
+    __half *out_f, *out_t;
+    HIP_CHECK(hipMalloc(&out_f, q_dim * 2));
+    HIP_CHECK(hipMalloc(&out_t, q_dim * 2));
+    HIP_CHECK(hipMemset(out_f, 0, q_dim * 2));
+    HIP_CHECK(hipMemset(out_t, 0, q_dim * 2));
+    const size_t cap = heads * ((cfg.max_seq_len + KV_CHUNK - 1) / KV_CHUNK);
+    float *po, *pm, *ps;
+    HIP_CHECK(hipMalloc(&po, cap * head_dim * 4));
+    HIP_CHECK(hipMalloc(&pm, cap * 4));
+    HIP_CHECK(hipMalloc(&ps, cap * 4));
+    auto fused = [&](hipGraphNode_t* an, hipGraphNode_t* mn) {
+        launch_rope_and_store_kv_decode(a_f, a_f + q_dim, a_f + q_dim + kv_dim,
+                                        fused_cache.get_k_cache(0), fused_cache.get_v_cache(0),
+                                        rope.d_cos, rope.d_sin, out_f, po, pm, ps, L, start_pos,
+                                        heads, kv_heads, head_dim, true, nullptr, an, mn);
+    };
+    hipGraphNode_t an = nullptr, mn = nullptr;
+    bool threw = false;
+    try {
+        fused(&an, &mn);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    HIP_CHECK(hipDeviceSynchronize());
+    bool untouched = same_bits(download(out_f, q_dim).data(), download(out_t, q_dim).data(),
+                               q_dim) &&
+                     same_bits(download(fused_cache.get_k_cache(0), cache_init.size()).data(),
+                               cache_init.data(), cache_init.size());
+    bool eager_ok = true;
+    try {
+        fused(nullptr, nullptr);
+    } catch (const std::runtime_error&) {
+        eager_ok = false;
+    }
+    launch_rope_and_store_kv(a_t, a_t + q_dim, a_t + q_dim + kv_dim, two_cache.get_k_cache(0),
+                             two_cache.get_v_cache(0), rope.d_cos, rope.d_sin, 1, heads, kv_heads,
+                             head_dim, 0, 0, start_pos, true, nullptr);
+    launch_causal_attention_decode(a_t, two_cache.get_k_cache(0), two_cache.get_v_cache(0), out_t,
+                                   po, pm, ps, 1, L, start_pos, heads, kv_heads, head_dim, 0, 0);
+    HIP_CHECK(hipDeviceSynchronize());
+    const bool same =
+        same_bits(download(out_f, q_dim).data(), download(out_t, q_dim).data(), q_dim) &&
+        same_bits(download(a_f, qkv.size()).data(), download(a_t, qkv.size()).data(),
+                  qkv.size()) &&
+        same_bits(download(fused_cache.get_k_cache(0), cache_init.size()).data(),
+                  download(two_cache.get_k_cache(0), cache_init.size()).data(),
+                  cache_init.size());
+    char detail[96];
+    std::snprintf(detail, sizeof detail, "threw=%d untouched=%d eager=%d same=%d", threw,
+                  untouched, eager_ok, same);
+    for (void* p : {(void*)a_f, (void*)a_t, (void*)out_f, (void*)out_t, (void*)po, (void*)pm,
+                    (void*)ps})
+        HIP_CHECK(hipFree(p));
+    report("fused_rope_decode_other_shape_throws_or_falls_back",
+           threw && untouched && eager_ok && same, detail);
+}
+
 }  // namespace
 
 int main() {
@@ -746,6 +824,7 @@ int main() {
     test_graph_fused_qkv_decode_step();
     test_graph_fused_rope_decode_step();
     test_qkv_gemm_prefill();
+    test_fused_rope_decode_other_shape();
     std::printf("%d failure(s)\n", g_failures);
     return g_failures;
 }

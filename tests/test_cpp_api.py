@@ -137,6 +137,27 @@ def test_node_updaters_exit_through_hip_check(tmp_path, call):
     assert "[HIP Error]" in r.stderr
 
 
+def test_rejected_launch_throws(tmp_path):
+    """A launch the library cannot serve is not silent: the launcher throws
+    std::runtime_error naming itself and the HIP error.  Null buffers with a
+    non-empty shape are rejected before any HIP call, so this runs anywhere."""
+    src = tmp_path / "rejected.cpp"
+    src.write_text('#include "kernels/kernels.hpp"\n#include <cstdio>\n#include <stdexcept>\n'
+                   "int main() {\n"
+                   "  try { launch_qkv_decode(nullptr, nullptr, nullptr, 2048, 3072); }\n"
+                   "  catch (const std::runtime_error& e) { std::puts(e.what()); return 3; }\n"
+                   "  std::puts(\"returned\"); return 0;\n}\n")
+    exe = tmp_path / "rejected"
+    lib_dir = ROOT / "llm-inference_amd" / "lib"
+    r = subprocess.run([HIPCC, "-std=c++23", "-I", str(ROOT / "include"), str(src), "-o", str(exe),
+                        "-L", str(lib_dir), "-lattn_mi355x", f"-Wl,-rpath,{lib_dir}"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 3, (r.returncode, r.stdout, r.stderr)
+    assert "launch_qkv_decode failed" in r.stdout and "returned" not in r.stdout
+
+
 @pytest.mark.gpu
 def test_cpp_reference_api_program(gpu):
     assert BIN.exists(), f"{BIN} not built: run __graft_entry__.build()"
@@ -144,7 +165,7 @@ def test_cpp_reference_api_program(gpu):
     print(r.stdout)
     print(r.stderr)
     lines = [l for l in r.stdout.splitlines() if l.startswith(("PASS", "FAIL"))]
-    assert len(lines) == 9, r.stdout + r.stderr
+    assert len(lines) == 10, r.stdout + r.stderr
     assert r.returncode == 0, r.stdout + r.stderr
 
 

@@ -151,22 +151,43 @@ def test_fused_graph_replays_with_node_updates(attn, gpu):
         hipgraph.destroy(graph, exe)
 
 
-def test_fused_rejects_shapes_off_the_mfma_path(attn, gpu):
-    """Shapes the fused kernels do not serve enqueue nothing and report
-    hipErrorInvalidValue (callers use the two launches)."""
+def test_fused_other_shapes_take_the_two_launches(attn, gpu):
+    """Shapes the fused kernels do not serve (start_pos outside the decoded
+    range, a padded kv_stride, head_dim 64): called eagerly they issue
+    attn_rope_store_kv then attn_decode (the same bits as those two calls);
+    asked for graph node handles they enqueue nothing and report
+    hipErrorInvalidValue, since only the fused pair can be patched."""
     L = 64
     q, k, v, cache, cos, sin, S = inputs(L, L - 1, seed=5)
-    st = State(attn, gpu, L, q, k, v, cache, cos, sin, S)
-    before = st.snapshot()
     lib = attn.lib()
+    sp = torch.cuda.current_stream().cuda_stream
     args = lambda **kw: dict(dict(L=L, pos=L - 1, D=D, kvs=0, hq=HQ, hkv=HKV), **kw)
-    for bad in (args(pos=L), args(kvs=KV_DIM + 8), args(D=64, kvs=0)):
-        rc = lib.attn_rope_store_kv_decode(
+
+    def call(st, bad, nodes):
+        an, mn = ctypes.c_void_p(), ctypes.c_void_p()
+        return lib.attn_rope_store_kv_decode(
             st.q.data_ptr(), st.k.data_ptr(), st.v.data_ptr(), st.kc, st.vc, st.cos.data_ptr(),
             st.sin.data_ptr(), st.out.data_ptr(), st.po.data_ptr(), st.pm.data_ptr(),
             st.ps.data_ptr(), bad["L"], bad["pos"], bad["hq"], bad["hkv"], bad["D"], bad["kvs"], 1,
-            torch.cuda.current_stream().cuda_stream, None, None)
-        assert rc == 1, (bad, rc)  # hipErrorInvalidValue
-    after = st.snapshot()
-    for x, y in zip(before, after):
-        assert np.array_equal(x, y)
+            sp, ctypes.byref(an) if nodes else None, ctypes.byref(mn) if nodes else None)
+
+    for bad in (args(pos=L), args(kvs=KV_DIM + 8), args(D=64, kvs=0)):
+        print(f"[case] fused rope+decode other shape {bad}", flush=True)
+        st = State(attn, gpu, L, q, k, v, cache, cos, sin, S)
+        before = st.snapshot()
+        assert call(st, bad, nodes=True) == 1, bad  # hipErrorInvalidValue
+        for x, y in zip(before, st.snapshot()):
+            assert np.array_equal(x, y)
+        assert call(st, bad, nodes=False) == 0, bad
+        got = st.snapshot()
+        ref = State(attn, gpu, L, q, k, v, cache, cos, sin, S)
+        assert lib.attn_rope_store_kv(ref.q.data_ptr(), ref.k.data_ptr(), ref.v.data_ptr(),
+                                      ref.kc, ref.vc, ref.cos.data_ptr(), ref.sin.data_ptr(), 1,
+                                      bad["hq"], bad["hkv"], bad["D"], 0, 0, bad["pos"], 1,
+                                      sp) == 0
+        assert lib.attn_decode(ref.q.data_ptr(), ref.kc, ref.vc, ref.out.data_ptr(),
+                               ref.po.data_ptr(), ref.pm.data_ptr(), ref.ps.data_ptr(), 1,
+                               bad["L"], bad["pos"], bad["hq"], bad["hkv"], bad["D"], 0,
+                               bad["kvs"], sp, None, None) == 0
+        for x, y in zip(got, ref.snapshot()):
+            assert np.array_equal(x, y), bad
