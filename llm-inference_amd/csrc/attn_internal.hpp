@@ -242,7 +242,8 @@ enum Option {
     kOptQkvGemmWide = 6,          // 0 = automatic; 1 = never; 2 = whenever the shape allows
     kOptPrefillWaves = 7,         // 0 = automatic; 4 or 8 waves per prefill workgroup
     kOptDecodeOutProjFused = 8,   // 1: attn_decode_out_proj runs the fused merge + o_proj kernel
-    kOptCount = 9
+    kOptPrefillStageAll = 9,      // 0 = automatic (N <= 256: all key tiles staged at once); 1 = never
+    kOptCount = 10
 };
 long get_option(int which);
 

@@ -25,8 +25,9 @@
 //    The V^T operand comes from row-major V through ds_read_b64_tr_b16 (two
 //    4-key transposing reads per operand), with the keys in the order the
 //    S^T accumulator produces them, so P never leaves registers.
-//  * Causal tile skipping: query tile i visits key tiles 0..i only; the
-//    diagonal tile is masked.  Tiles are handed out longest-first and the
+//  * Causal tile skipping: a workgroup's queries (64, or 32 for the 4-wave
+//    variant) visit only the 64-key tiles up to the one holding their last
+//    query; that tile, which crosses the diagonal, is masked.  Tiles are handed out longest-first and the
 //    four head groups of one KV head are kept on the same pair of XCDs so the
 //    KV head's K/V stays in one L2.
 //  * Tile j+1 is copied into the other LDS buffer while tile j is computed;
@@ -96,20 +97,34 @@ __device__ __forceinline__ bool map_block(uint32_t bid, uint32_t quads, uint32_t
 // fp16 and the O^T accumulators are rarely touched by VALU code.
 constexpr float kRescaleSlack = 8.0f;
 
+// Key tiles an ALL workgroup stages at once: 4 x (17,408 + 20,480) B of LDS
+constexpr uint32_t kAllTiles = 4;
+
 // WAVES = 8: 64 queries of 4 heads per workgroup, two waves per SIMD (long
 // prompts); WAVES = 4: 32 queries of 4 heads, one wave per SIMD, so a short
 // prompt's few workgroups each finish their chain of key tiles sooner.
-template <int WAVES>
+// ALL (WAVES = 4, at most kAllTiles key tiles, i.e. N <= 256): every key tile
+// the workgroup needs is copied into LDS at once and awaited once, instead of
+// one tile ahead of the compute.  A short prompt's chain of tiles is
+// otherwise bound by the copy latency, not by the compute: per-wave
+// timestamps at N = 254 showed ~1.9 us per tile (the next tile's copy,
+// issued at the start of a tile, completing after the tile's compute)
+// against ~0.8 us per tile once the copies hit L2 at N = 1024.
+template <int WAVES, bool ALL>
 __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
+    static_assert(!ALL || WAVES == 4, "the all-tiles variant is the 4-wave kernel");
     constexpr int kW = WAVES;
     constexpr int kBMw = 8 * WAVES;                     // query tokens per workgroup
     constexpr int kDpw = (kVDma + WAVES - 1) / WAVES;   // DMA instructions per wave
     // two LDS buffers per operand as distinct objects, so the compiler can
-    // tell a DMA into one buffer from the reads of the other
-    __shared__ __attribute__((aligned(16))) f16 kt0[kBN * kKP];
-    __shared__ __attribute__((aligned(16))) f16 kt1[kBN * kKP];
-    __shared__ __attribute__((aligned(16))) f16 vt0[kBN * kVP];
-    __shared__ __attribute__((aligned(16))) f16 vt1[kBN * kVP];
+    // tell a DMA into one buffer from the reads of the other (ALL: one buffer
+    // per key tile, all filled before any is read)
+    constexpr int kKBuf = ALL ? (int)kAllTiles * kBN * kKP : kBN * kKP;
+    constexpr int kVBuf = ALL ? (int)kAllTiles * kBN * kVP : kBN * kVP;
+    __shared__ __attribute__((aligned(16))) f16 kt0[kKBuf];
+    __shared__ __attribute__((aligned(16))) f16 kt1[ALL ? 8 : kBN * kKP];
+    __shared__ __attribute__((aligned(16))) f16 vt0[kVBuf];
+    __shared__ __attribute__((aligned(16))) f16 vt1[ALL ? 8 : kBN * kVP];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -272,6 +287,16 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         l_run += psum;
     };
 
+    if constexpr (ALL) {
+        // tiles 0..last (last < kAllTiles) side by side, one wait
+        for (uint32_t t = 0; t <= last; ++t)
+            stage(t * kBN, kt0 + t * (kBN * kKP), vt0 + t * (kBN * kVP));
+        publish();
+#pragma unroll 1
+        for (uint32_t t = 0; t < last; ++t)
+            tile_step(kt0 + t * (kBN * kKP), vt0 + t * (kBN * kVP), t, std::false_type{});
+        tile_step(kt0 + last * (kBN * kKP), vt0 + last * (kBN * kVP), last, std::true_type{});
+    } else {
     // Tile t sits in buffer t & 1.  Full tiles 0..last-1 need no mask; tile
     // `last` holds the diagonal.  The DMA of tile j+1 goes into the buffer
     // last read before the previous barrier.
@@ -293,6 +318,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         tile_step(kt1, vt1, last, std::true_type{});
     } else {
         tile_step(kt0, vt0, last, std::true_type{});
+    }
     }
 
     // ---- epilogue: O = O^T / l, packed [N][Hq][D]
@@ -352,10 +378,17 @@ hipError_t launch_prefill_kernel(const PrefillArgs& a0, int path, hipStream_t st
         blocks = (uint64_t)a.q_tiles * quads;
     }
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
-    if (waves == 4)
-        hipLaunchKernelGGL(prefill_d128<4>, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+    const bool all = waves == 4 && a.seq_len <= kAllTiles * kBN &&
+                     get_option(kOptPrefillStageAll) != 1;
+    if (all)
+        hipLaunchKernelGGL((prefill_d128<4, true>), dim3((uint32_t)blocks), dim3(256), 0, stream,
+                           a);
+    else if (waves == 4)
+        hipLaunchKernelGGL((prefill_d128<4, false>), dim3((uint32_t)blocks), dim3(256), 0, stream,
+                           a);
     else
-        hipLaunchKernelGGL(prefill_d128<8>, dim3((uint32_t)blocks), dim3(512), 0, stream, a);
+        hipLaunchKernelGGL((prefill_d128<8, false>), dim3((uint32_t)blocks), dim3(512), 0, stream,
+                           a);
     return hipGetLastError();
 }
 
