@@ -212,6 +212,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
     // one 64-key tile: S^T = K . Q^T, online softmax, O^T += V^T . P^T
     auto tile_step = [&](const f16* kt, const f16* vt, uint32_t j, auto diag_tag) {
         constexpr bool kDiag = decltype(diag_tag)::value;
+        // the compiler's interleaving strategy for LDS reads and MFMAs
+        // (iglp_opt 0): 8-wave tile at C4 261.7 against 265.8 us (median of
+        // six 100-launch medians each, same box), identical bits
+        if constexpr (WAVES == 8) __builtin_amdgcn_iglp_opt(0);
         f32x16 s[2] = {f32x16{}, f32x16{}};
         // K operands are read one k-step ahead of their MFMAs
         const f16* kb = kt + n * kKP + 8 * hh;
