@@ -123,18 +123,28 @@ def test_prefill_8192_vs_oracle_rows_and_torch(attn, gpu):
     assert_close(got, ref, 2e-3, 1e-2, "torch fp32")
 
 
-def test_prefill_prefix_invariance(attn, gpu):
-    # row t depends only on rows <= t: a prefill of N tokens and of a prefix of
-    # N' tokens agree bit for bit on the first N' rows
-    N = 700
+@pytest.mark.parametrize("N,prefixes,split_keys", [(700, (1, 64, 65, 333), 1),
+                                                   (254, (1, 31, 64, 65, 200), 0)])
+def test_prefill_prefix_invariance(attn, gpu, N, prefixes, split_keys):
+    """Row t depends only on rows <= t: a prefill of N tokens and of a prefix
+    of N' tokens agree bit for bit on the first N' rows -- across the
+    pipelined and all-tiles-staged kernels (which compute the same tiles in
+    the same order; the split-keys form is off), and within the split-keys
+    form of short prompts (the same tiles combined the same way)."""
     qkv, cache, stride = engine_inputs(N, seed=21)
-    full = run_prefill(attn, gpu, qkv, cache, N, stride).reshape(N, -1)
-    for Np in (1, 64, 65, 333):
-        q2, c2, _ = engine_inputs(N, seed=21)
-        c2 = np.concatenate([c2[:(N + 2) * 512].reshape(N + 2, 512)[:Np + 2].reshape(-1),
-                             c2[(N + 2) * 512:].reshape(N + 2, 512)[:Np + 2].reshape(-1)])
-        part = run_prefill(attn, gpu, q2[:Np * stride], c2, Np, stride).reshape(Np, -1)
-        assert np.array_equal(part, full[:Np]), Np
+    try:
+        attn.set_option("prefill_split_keys", split_keys)
+        full = run_prefill(attn, gpu, qkv, cache, N, stride).reshape(N, -1)
+        for Np in prefixes:
+            print(f"[case] prefill prefix N={N} N'={Np} split_keys={'off' if split_keys else 'auto'}",
+                  flush=True)
+            q2, c2, _ = engine_inputs(N, seed=21)
+            c2 = np.concatenate([c2[:(N + 2) * 512].reshape(N + 2, 512)[:Np + 2].reshape(-1),
+                                 c2[(N + 2) * 512:].reshape(N + 2, 512)[:Np + 2].reshape(-1)])
+            part = run_prefill(attn, gpu, q2[:Np * stride], c2, Np, stride).reshape(Np, -1)
+            assert np.array_equal(part, full[:Np]), Np
+    finally:
+        attn.set_option("prefill_split_keys", 0)
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,extra", [(16, 4, 64, 0), (16, 16, 128, 0), (8, 2, 128, 8),
@@ -219,14 +229,36 @@ def test_prefill_four_and_eight_wave_tiles_identical(attn, gpu, N):
     qkv, cache, stride = engine_inputs(N, seed=700 + N)
     outs = {}
     try:
+        # the split-keys form of short prompts combines tiles in another order
+        attn.set_option("prefill_split_keys", 1)
         for waves in (4, 8):
             attn.set_option("prefill_waves", waves)
             print(f"[case] prefill N={N} waves={waves}", flush=True)
             outs[waves] = run_prefill(attn, gpu, qkv, cache, N, stride)
     finally:
         attn.set_option("prefill_waves", 0)
+        attn.set_option("prefill_split_keys", 0)
     assert np.array_equal(outs[4], outs[8])
     rows = None if N <= 1024 else np.unique(np.concatenate([np.arange(0, N, 7), [N - 1]]))
     exp = oracle_prefill(qkv, cache, N, stride, rows=rows).reshape(-1)
     got = outs[4] if rows is None else outs[4].reshape(N, -1)[rows].reshape(-1)
     assert_close(got, exp, 2e-3, 1e-2, f"N={N}")
+
+
+@pytest.mark.parametrize("N", [1, 2, 31, 32, 33, 63, 64, 65, 96, 97, 128, 129, 191, 192, 200,
+                               254, 255, 256])
+def test_prefill_split_keys_vs_oracle(attn, gpu, N):
+    """Short prompts (N <= 256): one workgroup per head and 32-query tile,
+    its key tiles computed by different waves and combined through LDS;
+    against the fp64 oracle, and against the sequential kernel (the same
+    attention, combined in another order: within the tolerance)."""
+    qkv, cache, stride = engine_inputs(N, seed=1300 + N)
+    print(f"[case] prefill split keys N={N}", flush=True)
+    got = run_prefill(attn, gpu, qkv, cache, N, stride)
+    assert_close(got, oracle_prefill(qkv, cache, N, stride).reshape(-1), 2e-3, 1e-2, f"N={N}")
+    try:
+        attn.set_option("prefill_split_keys", 1)
+        seq = run_prefill(attn, gpu, qkv, cache, N, stride)
+    finally:
+        attn.set_option("prefill_split_keys", 0)
+    assert_close(got, seq, 2e-3, 1e-2, f"N={N} vs sequential tiles")
