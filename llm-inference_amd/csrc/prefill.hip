@@ -350,27 +350,34 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
             // tile leave (O^T, m, l) in LDS over the K tiles; then wave w folds
             // the 32 output dims 32 w .. 32 w + 31 of every state and stores
             // them, so the epilogue's work is split four ways.
+            // State of wave t in LDS, 16-byte words per lane: [t][17][64] x
+            // f32x4 = 17,408 B per wave (words 0-15: O^T of dims 32 dt + ...,
+            // word 16: (m, l))
             __syncthreads();  // every wave has finished reading K and V
-            float* st = reinterpret_cast<float*>(kt0);  // [4][66][64] floats (67,584 B)
+            f32x4* st = reinterpret_cast<f32x4*>(kt0);  // [4][17][64] (69,632 B)
             if (t <= last) {
-                float* w = st + t * (66u * 64u) + (uint32_t)lane;
+                f32x4* w = st + t * (17u * 64u) + (uint32_t)lane;
 #pragma unroll
-                for (int e = 0; e < 64; ++e) w[64 * e] = o[e >> 4][e & 15];
-                w[64 * 64] = m_used;
-                w[64 * 65] = l_run;
+                for (int e = 0; e < 16; ++e)
+                    w[64 * e] = f32x4{o[e >> 2][4 * (e & 3)], o[e >> 2][4 * (e & 3) + 1],
+                                      o[e >> 2][4 * (e & 3) + 2], o[e >> 2][4 * (e & 3) + 3]};
+                w[64 * 16] = f32x4{m_used, l_run, 0.f, 0.f};
             }
             __syncthreads();
             const int dt = wave;
             float m = -INFINITY, l = 0.f;
             f32x16 acc = f32x16{};
             for (uint32_t w2 = 0; w2 <= last; ++w2) {
-                const float* w = st + w2 * (66u * 64u) + (uint32_t)lane;
-                const float m2 = w[64 * 64];
-                const float mx = fmaxf(m, m2);  // finite: m2 is
-                const float a1 = fast_exp2(m - mx), a2 = fast_exp2(m2 - mx);
-                l = l * a1 + w[64 * 65] * a2;
+                const f32x4* w = st + w2 * (17u * 64u) + (uint32_t)lane;
+                const f32x4 ml = w[64 * 16];
+                f32x4 ow[4];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) acc[i] = acc[i] * a1 + w[64 * (16 * dt + i)] * a2;
+                for (int q = 0; q < 4; ++q) ow[q] = w[64 * (4 * dt + q)];
+                const float mx = fmaxf(m, ml[0]);  // finite: ml[0] is
+                const float a1 = fast_exp2(m - mx), a2 = fast_exp2(ml[0] - mx);
+                l = l * a1 + ml[1] * a2;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[i] = acc[i] * a1 + ow[i >> 2][i & 3] * a2;
                 m = mx;
             }
             const float inv = 1.f / (l + xor_lane(l, 32));
