@@ -116,7 +116,7 @@ constexpr uint32_t kAllTiles = 4;
 // combined through LDS (M = max(m_a, m_b); l and O scaled by 2^(m - M) and
 // added), so the chain of up to 4 dependent tiles becomes one tile plus the
 // combine, and a short prompt gets 4x the workgroups (one per head instead
-// of per 4 heads): C2 (254 tokens) 10.1 -> 6.8 us, 64 tokens 6.3 -> 4.7 us.
+// of per 4 heads): C2 (254 tokens) 10.1 -> 6.6 us, 64 tokens 6.3 -> 4.7 us.
 template <int WAVES, bool ALL, bool SK>
 __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
     static_assert(!ALL || WAVES == 4, "the all-tiles variant is the 4-wave kernel");
