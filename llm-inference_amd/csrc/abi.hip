@@ -499,17 +499,19 @@ int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16
     // token inside the decoded range
     const bool al = ((uintptr_t)k | (uintptr_t)v | (uintptr_t)cos_table | (uintptr_t)sin_table |
                      (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0;
+    const bool host_ok = al && kvs == kv_dim && start_pos < kv_len;
+    // Other shapes: eager calls issue the two launches this replaces; a
+    // capture asking for node handles is rejected (hipErrorInvalidValue,
+    // nothing enqueued), because attn_update_rope_decode_nodes could not
+    // patch that sequence as one pair
+    if (!host_ok && (attention_node || merge_node)) return (int)hipErrorInvalidValue;
     int device = 0;
     hipError_t e = hipGetDevice(&device);
     if (e != hipSuccess) return (int)e;
     const DecodePlan p = plan_decode((uint32_t)kv_len, (uint32_t)num_heads,
                                      (uint32_t)num_kv_heads, (uint32_t)head_dim, kvs, q,
                                      k_cache, v_cache, device);
-    if (p.path == 0 || !al || kvs != kv_dim || start_pos >= kv_len) {
-        // Other shapes: eager calls issue the two launches this replaces;
-        // a capture asking for node handles is rejected (hipErrorInvalidValue,
-        // nothing enqueued), because attn_update_rope_decode_nodes could not
-        // patch that sequence as one pair
+    if (p.path == 0 || !host_ok) {
         if (attention_node || merge_node) return (int)hipErrorInvalidValue;
         const int rc = attn_rope_store_kv(q, const_cast<attn_f16_t*>(k), v, k_cache, v_cache,
                                           cos_table, sin_table, 1, num_heads, num_kv_heads,

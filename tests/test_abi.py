@@ -105,18 +105,43 @@ def test_invalid_arguments_are_errors(attn):
     assert lib.attn_qkv_rope_store_kv_decode(16, y, 16, 16, 16, None, 16, 2048, 16, 4, 128, 0, 1,
                                              None) != 0
     assert lib.attn_update_qkv_rope_node(None, None, 0, 1) != 0
-    # fused RoPE + decode: null pointers, missing tables when rotating, cache
-    # rows not kv_dim apart, the new token outside the decoded range
+    # fused RoPE + decode: null pointers, missing tables when rotating; and,
+    # when graph node handles are requested (the pair must be patchable), cache
+    # rows not kv_dim apart or the new token outside the decoded range are
+    # rejected with hipErrorInvalidValue before any HIP call
     p = [16] * 11
-    def fused(ptrs, L=64, pos=63, kvs=0, apply=1):
-        return lib.attn_rope_store_kv_decode(*ptrs, L, pos, 16, 4, 128, kvs, apply, None, None,
-                                             None)
+    an, mn = ctypes.c_void_p(), ctypes.c_void_p()
+    def fused(ptrs, L=64, pos=63, kvs=0, apply=1, nodes=False):
+        return lib.attn_rope_store_kv_decode(
+            *ptrs, L, pos, 16, 4, 128, kvs, apply, None,
+            ctypes.byref(an) if nodes else None, ctypes.byref(mn) if nodes else None)
     assert fused([None] + p[1:]) != 0
     assert fused(p[:5] + [None] + p[6:]) != 0
-    assert fused(p, kvs=520) != 0
-    assert fused(p, pos=64) != 0
+    assert fused(p, kvs=520, nodes=True) == 1  # hipErrorInvalidValue
+    assert fused(p, pos=64, nodes=True) == 1
+    assert fused([16] * 4 + [24] + [16] * 6, nodes=True) == 1  # a cache pointer not 16-byte aligned
     assert lib.attn_update_rope_decode_nodes(None, None, None, 64, 64, 1) != 0
     assert lib.attn_update_rope_decode_nodes(None, None, None, 0, 0, 1) != 0
+
+
+def test_out_projection_host_rules(attn):
+    """launch_attention_out_projection_decode and the decode + o_proj entry
+    point: the no-op and error rules that need no GPU, and the workspace
+    size (fp32 head partials rounded up to 256 bytes, then one uint32 counter
+    per 128 output rows)."""
+    lib = attn.lib()
+    # hidden_size == 0 launches nothing, even with null pointers
+    # (matrix_vec_mul.hip.cpp:160)
+    assert lib.attn_out_proj_decode(None, None, None, 0, 16, 128, 1.0, None) == 0
+    # null operands with a non-empty projection
+    assert lib.attn_out_proj_decode(None, None, None, 2048, 16, 128, 1.0, None) != 0
+    assert lib.attn_out_proj_decode(None, 16, None, 2048, 16, 128, 1.0, None) != 0
+    # decode + o_proj with kv_len 0 and hidden 0: both replaced launches are no-ops
+    assert lib.attn_decode_out_proj(*([None] * 7), 0, 16, 4, 128, 0, None, None, 0, 1.0, None,
+                                    None, None, None) == 0
+    for Hq, hidden in ((16, 2048), (16, 2000), (12, 100), (1, 1)):
+        part = (Hq * hidden * 4 + 255) // 256 * 256
+        assert lib.attn_decode_out_proj_workspace_bytes(Hq, hidden) == part + 4 * ((hidden + 127) // 128)
 
 
 def test_decode_plan_respects_workspace_capacity(attn):
