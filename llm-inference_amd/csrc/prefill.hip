@@ -32,6 +32,10 @@
 //    KV head's K/V stays in one L2.
 //  * Tile j+1 is copied into the other LDS buffer while tile j is computed;
 //    one barrier per tile.
+//  * Short prompts (N <= 256) split each 32-query tile's keys over the waves
+//    of one head's workgroup and combine the partial states through LDS
+//    (prefill_d128<4, true, true>: 64-key tiles over 4 waves; prefill_sk32:
+//    32-key units over 8 waves, up to 32 tokens).
 #include "attn_internal.hpp"
 
 #include <type_traits>
@@ -448,6 +452,200 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
     }
 }
 
+// Split keys over 8 waves of 32 keys each (N <= 256).  A workgroup is ONE
+// head's 32-query tile (queries 32 t .. 32 t + 31, keys 0 .. 32 t + 31); wave
+// w owns key unit w (keys 32 w .. 32 w + 31) if w <= t.  Each wave copies its
+// K unit (32 rows at pitch kKP: 9 DMA instructions, the last half of the
+// ninth re-fetching row 0 into padding) and V unit (32 rows at pitch kVP: 10
+// instructions) into its own 19 KiB LDS region, waits for its own copy, and
+// computes S^T, the exact maximum of its 32 keys (one unit per wave, so no
+// running rescale), P and O^T.  Its state (O^T, m, l) then overwrites its own
+// region; after one barrier wave w folds output dims 32 (w / 2) + 8 i4 +
+// 4 hh + 0..3 for i4 = 2 (w % 2), 2 (w % 2) + 1 over the states
+// (M = max m, l and O scaled by 2^(m - M) and added) and stores them.
+// Against the 4-wave form (one 64-key tile per wave): half the copy and half
+// the dependent MFMA chain per wave on the critical path, two waves per SIMD,
+// but twice the states to combine (16 KiB of fp32 O^T per unit, written
+// and read back through LDS).
+constexpr int kSkUnit = 32;                            // keys per wave
+constexpr int kSkWaves = 8;                            // units per query tile, at most
+constexpr int kSkKDma = 9;                             // 32 x 17 chunks = 8.5 KiB, rounded up
+constexpr int kSkVDma = kSkUnit * kVChunks / 64;       // 10
+constexpr int kSkRegion = (kSkKDma + kSkVDma) * 1024;  // 19,456 B per wave
+constexpr uint32_t kSkMaxTokens = kSkWaves * kSkUnit;  // 256
+
+__global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) char lds[kSkWaves * kSkRegion];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 31;
+    const int hh = lane >> 5;
+    uint32_t head, tile;
+    if (!map_block(blockIdx.x, a.num_heads, a.q_tiles, head, tile)) return;
+    const uint32_t last = tile;  // the query tile's diagonal unit
+    // one unit: wave 0 holds the whole state and finishes it alone
+    if (last == 0 && wave != 0) return;
+    const uint32_t u = (uint32_t)wave;
+    const uint32_t g = head / a.group;
+    const uint32_t q0 = tile * (uint32_t)kSkUnit;
+    const uint32_t N = a.seq_len;
+    const uint32_t kv_row_bytes = (uint32_t)(a.kv_stride * 2);
+    char* region = lds + u * kSkRegion;
+
+    f32x16 o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
+    float m_unit = -INFINITY, l_unit = 0.f;
+    if (u <= last) {
+        // the unit's rows start at kv0 < N (kv0 <= q0 and tile t exists only
+        // if q0 < N); rows past N read as zero
+        const uint32_t kv0 = u * (uint32_t)kSkUnit;
+        const uint32_t bytes = __builtin_amdgcn_readfirstlane((N - kv0 - 1u) * kv_row_bytes + kD * 2);
+        const BufRsrc rk = make_rsrc(a.k + (uint64_t)kv0 * a.kv_stride + (uint64_t)g * kD, bytes);
+        const BufRsrc rv = make_rsrc(a.v + (uint64_t)kv0 * a.kv_stride + (uint64_t)g * kD, bytes);
+#pragma unroll
+        for (int i = 0; i < kSkKDma; ++i) {
+            const uint32_t q = (uint32_t)i * 64u + (uint32_t)lane;
+            const uint32_t kr = q / kKChunks, kc = q % kKChunks;
+            const uint32_t off = q < (uint32_t)(kSkUnit * kKChunks)
+                                     ? kr * kv_row_bytes + (kc < 16 ? kc : 0u) * 16u
+                                     : 0u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rk, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)region + 1024 * i), 16, (int)off, 0,
+                0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < kSkVDma; ++i) {
+            const uint32_t q = (uint32_t)i * 64u + (uint32_t)lane;
+            const uint32_t vr = q / kVChunks, vc = q % kVChunks;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rv, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)region + 1024 * (kSkKDma + i)), 16,
+                (int)(vr * kv_row_bytes + (vc < 16 ? vc : 0u) * 16u), 0, 0, 0);
+        }
+        // Q^T B operands (lane (hh, n): Q[q0 + n][head][16 s + 8 hh .. +7]),
+        // loaded while the copy is in flight; rows past N read as zero
+        const uint32_t q_row_bytes = (uint32_t)(a.q_stride * 2);
+        const BufRsrc rq = make_rsrc(a.q + (uint64_t)head * kD,
+                                     __builtin_amdgcn_readfirstlane((N - 1) * q_row_bytes + kD * 2));
+        f16x8 qb[8];
+        const uint32_t qoff = (q0 + n) * q_row_bytes + 16u * hh;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) qb[s] = buf_ld16(rq, qoff + 32u * s);
+        // a wave sees its own LDS-DMA writes once vmcnt reaches 0
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+
+        const f16* kt = reinterpret_cast<const f16*>(region);
+        const f16* vt = reinterpret_cast<const f16*>(region + kSkKDma * 1024);
+        // S^T = K . Q^T: lane (hh, n) holds keys 8 (i / 4) + 4 hh + i % 4 of
+        // the unit for query n
+        f32x16 s = f32x16{};
+        const f16* kb = kt + n * kKP + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) s = mfma32(lds16(kb + 16 * ks), qb[ks], s);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float x = s[i];
+            if (u == last) {
+                // the diagonal unit starts at q0: mask keys past the query and past N
+                const uint32_t key = q0 + 8u * (uint32_t)(i >> 2) + 4u * hh + (uint32_t)(i & 3);
+                if (key > q0 + n || key >= N) x = -INFINITY;
+                s[i] = x;
+            }
+            mx = fmaxf(mx, x);
+        }
+        // finite: key kv0 <= q0 <= every query of the tile, and kv0 < N
+        mx = fmaxf(mx, xor_lane(mx, 32));
+        m_unit = mx * a.scale_log2;
+        const float mneg = -m_unit;
+        const uint32_t grp = (uint32_t)lane >> 4, jl = (uint32_t)lane & 15u;
+        const f16* vb = vt + (4u * hh + (jl >> 2)) * kVP + 16u * (grp & 1u) + 4u * (jl & 3u);
+        float psum = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            f16x8 va[4];
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const f16x4 lo = lds_tr4(vb + 16 * ks * kVP + 32 * dt);
+                const f16x4 hi = lds_tr4(vb + (16 * ks + 8) * kVP + 32 * dt);
+                va[dt] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+            f16x8 pb;
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                pb[r] = (f16)fast_exp2(__builtin_fmaf(s[8 * ks + r], a.scale_log2, mneg));
+#pragma unroll
+            for (int r = 0; r < 8; r += 2) {
+                const f16x2 pair = {pb[r], pb[r + 1]};
+                psum = __builtin_amdgcn_fdot2(pair, f16x2{(f16)1.0f, (f16)1.0f}, psum, false);
+            }
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[dt] = mfma32(va[dt], pb, o[dt]);
+        }
+        l_unit = psum;
+    }
+    const uint32_t query = q0 + n;
+    if (last == 0) {
+        const float inv = 1.f / (l_unit + xor_lane(l_unit, 32));
+        if (query < N) {
+            f16* orow = a.out + ((uint64_t)query * a.num_heads + head) * kD;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    f16x4 w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[e] = (f16)(o[dt][4 * i4 + e] * inv);
+                    *reinterpret_cast<f16x4*>(orow + 32 * dt + 8 * i4 + 4 * hh) = w;
+                }
+        }
+        return;
+    }
+    // state of unit u over its own region, 16-byte words per lane: words
+    // 0-15 O^T (word e = o[e / 4][4 (e % 4) .. +3]), word 16 (m, l); the
+    // wave's own LDS reads of the region precede these writes in order
+    if (u <= last) {
+        f32x4* w = reinterpret_cast<f32x4*>(region) + lane;
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            w[64 * e] = f32x4{o[e >> 2][4 * (e & 3)], o[e >> 2][4 * (e & 3) + 1],
+                              o[e >> 2][4 * (e & 3) + 2], o[e >> 2][4 * (e & 3) + 3]};
+        w[64 * 16] = f32x4{m_unit, l_unit, 0.f, 0.f};
+    }
+    __syncthreads();
+    const int dt = wave >> 1;
+    const int e0 = 4 * dt + 2 * (wave & 1);  // this wave's two state words
+    float m = -INFINITY, l = 0.f;
+    f32x4 acc[2] = {f32x4{}, f32x4{}};
+    for (uint32_t w2 = 0; w2 <= last; ++w2) {
+        const f32x4* w = reinterpret_cast<const f32x4*>(lds + w2 * kSkRegion) + lane;
+        const f32x4 ml = w[64 * 16];
+        const f32x4 o0 = w[64 * e0], o1 = w[64 * (e0 + 1)];
+        const float mx = fmaxf(m, ml[0]);  // ml[0] is finite
+        const float a1 = fast_exp2(m - mx), a2 = fast_exp2(ml[0] - mx);
+        l = l * a1 + ml[1] * a2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            acc[0][e] = acc[0][e] * a1 + o0[e] * a2;
+            acc[1][e] = acc[1][e] * a1 + o1[e] * a2;
+        }
+        m = mx;
+    }
+    const float inv = 1.f / (l + xor_lane(l, 32));
+    if (query < N) {
+        f16* orow = a.out + ((uint64_t)query * a.num_heads + head) * kD;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i4 = 2 * (wave & 1) + k;
+            f16x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = (f16)(acc[k][e] * inv);
+            *reinterpret_cast<f16x4*>(orow + 32 * dt + 8 * i4 + 4 * hh) = w;
+        }
+    }
+}
+
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -489,8 +687,21 @@ hipError_t launch_prefill_kernel(const PrefillArgs& a0, int path, hipStream_t st
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
     const bool all = waves == 4 && a.seq_len <= kAllTiles * kBN &&
                      get_option(kOptPrefillStageAll) != 1;
-    const bool sk = all && get_option(kOptPrefillSplitKeys) != 1;
-    if (sk) {
+    const long sk_opt = get_option(kOptPrefillSplitKeys);
+    const bool sk = all && sk_opt != 1;
+    // 32-key units over 8 waves only where one query tile needs no combine
+    // (N <= 32: 4.1 against 4.6 us per graph launch); with several units
+    // their 8 fp32 states cost twice the LDS traffic of the 4-wave form's
+    // (N = 254: 7.1 against 6.6 us)
+    const bool sk32 = sk && (sk_opt == 3 || (sk_opt != 2 && a.seq_len <= kSkUnit)) &&
+                      a.seq_len <= kSkMaxTokens;
+    if (sk32) {
+        // one 8-wave workgroup per (head, 32-query tile), 32 keys per wave
+        PrefillArgs b = a0;
+        b.q_tiles = (b.seq_len + kSkUnit - 1) / kSkUnit;
+        hipLaunchKernelGGL(prefill_sk32, dim3(b.q_tiles * b.num_heads), dim3(64 * kSkWaves), 0,
+                           stream, b);
+    } else if (sk) {
         // one workgroup per (head, 32-query tile)
         const uint64_t sk_blocks = (uint64_t)a.q_tiles * a.num_heads;
         if (sk_blocks > 0x7fffffffull) return hipErrorInvalidValue;

@@ -124,20 +124,21 @@ def test_prefill_8192_vs_oracle_rows_and_torch(attn, gpu):
 
 
 @pytest.mark.parametrize("N,prefixes,split_keys", [(700, (1, 64, 65, 333), 1),
-                                                   (254, (1, 31, 64, 65, 200), 0)])
+                                                   (254, (1, 31, 64, 65, 200), 2),
+                                                   (254, (1, 31, 64, 65, 200), 3)])
 def test_prefill_prefix_invariance(attn, gpu, N, prefixes, split_keys):
     """Row t depends only on rows <= t: a prefill of N tokens and of a prefix
     of N' tokens agree bit for bit on the first N' rows -- across the
     pipelined and all-tiles-staged kernels (which compute the same tiles in
-    the same order; the split-keys form is off), and within the split-keys
-    form of short prompts (the same tiles combined the same way)."""
+    the same order; the split-keys form is off), and within each split-keys
+    form of short prompts (option value 2: 64-key tiles over 4 waves, 3:
+    32-key units over 8 waves; the same units combined the same way)."""
     qkv, cache, stride = engine_inputs(N, seed=21)
     try:
         attn.set_option("prefill_split_keys", split_keys)
         full = run_prefill(attn, gpu, qkv, cache, N, stride).reshape(N, -1)
         for Np in prefixes:
-            print(f"[case] prefill prefix N={N} N'={Np} split_keys={'off' if split_keys else 'auto'}",
-                  flush=True)
+            print(f"[case] prefill prefix N={N} N'={Np} split_keys={split_keys}", flush=True)
             q2, c2, _ = engine_inputs(N, seed=21)
             c2 = np.concatenate([c2[:(N + 2) * 512].reshape(N + 2, 512)[:Np + 2].reshape(-1),
                                  c2[(N + 2) * 512:].reshape(N + 2, 512)[:Np + 2].reshape(-1)])
@@ -245,20 +246,49 @@ def test_prefill_four_and_eight_wave_tiles_identical(attn, gpu, N):
     assert_close(got, exp, 2e-3, 1e-2, f"N={N}")
 
 
+@pytest.mark.parametrize("form", [0, 2, 3])
 @pytest.mark.parametrize("N", [1, 2, 31, 32, 33, 63, 64, 65, 96, 97, 128, 129, 191, 192, 200,
                                254, 255, 256])
-def test_prefill_split_keys_vs_oracle(attn, gpu, N):
+def test_prefill_split_keys_vs_oracle(attn, gpu, N, form):
     """Short prompts (N <= 256): one workgroup per head and 32-query tile,
-    its key tiles computed by different waves and combined through LDS;
+    its keys split over the waves (form 2: 64-key tiles over 4 waves; form
+    3: 32-key units over 8 waves; form 0, the default: form 3 up to 32
+    tokens, form 2 above) and combined through LDS;
     against the fp64 oracle, and against the sequential kernel (the same
     attention, combined in another order: within the tolerance)."""
     qkv, cache, stride = engine_inputs(N, seed=1300 + N)
-    print(f"[case] prefill split keys N={N}", flush=True)
-    got = run_prefill(attn, gpu, qkv, cache, N, stride)
-    assert_close(got, oracle_prefill(qkv, cache, N, stride).reshape(-1), 2e-3, 1e-2, f"N={N}")
+    print(f"[case] prefill split keys N={N} form={form}", flush=True)
     try:
+        attn.set_option("prefill_split_keys", form)
+        got = run_prefill(attn, gpu, qkv, cache, N, stride)
         attn.set_option("prefill_split_keys", 1)
         seq = run_prefill(attn, gpu, qkv, cache, N, stride)
     finally:
         attn.set_option("prefill_split_keys", 0)
+    assert_close(got, oracle_prefill(qkv, cache, N, stride).reshape(-1), 2e-3, 1e-2, f"N={N}")
     assert_close(got, seq, 2e-3, 1e-2, f"N={N} vs sequential tiles")
+
+
+@pytest.mark.parametrize("Hq,Hkv,N", [(8, 2, 256), (4, 1, 100), (32, 4, 97), (16, 2, 255)])
+def test_prefill_split_keys_other_heads(attn, gpu, Hq, Hkv, N):
+    """The split-keys forms at other head counts (4 and 8 query heads take
+    the XCD-pinned block order, 16 and 32 the plain one) and with padded row
+    strides, against the fp64 oracle."""
+    D = 128
+    q_stride, kv_stride = Hq * D + 8, Hkv * D + 24
+    rng = np.random.default_rng(Hq * 1000 + N)
+    q = rng.standard_normal(N * q_stride).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((N + 1) * kv_stride).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((N + 1) * kv_stride).astype(np.float16).view(np.uint16)
+    _, e32 = oracle.attention(q, k, v, N, Hq, Hkv, D, q_stride, kv_stride, N, causal=True)
+    try:
+        for form in (2, 3):
+            attn.set_option("prefill_split_keys", form)
+            print(f"[case] prefill split keys Hq={Hq} Hkv={Hkv} N={N} form={form}", flush=True)
+            out = torch.empty(N * Hq * D, dtype=torch.float16, device=gpu)
+            attn.prefill(dev(q, gpu), dev(k, gpu), dev(v, gpu), out, N, Hq, Hkv, D, q_stride,
+                         kv_stride)
+            torch.cuda.synchronize()
+            assert_close(host(out), e32.reshape(-1), 2e-3, 1e-2, f"{Hq}/{Hkv} N={N} form={form}")
+    finally:
+        attn.set_option("prefill_split_keys", 0)
