@@ -146,7 +146,23 @@ def bench_lib():
     lib.attn_bench_read2.restype = ctypes.c_int
     lib.attn_bench_engine_decode.argtypes = [vp] * 8 + [sz] * 7 + [ctypes.c_int, vp]
     lib.attn_bench_engine_decode.restype = ctypes.c_int
+    lib.attn_bench_empty.argtypes = [vp, ctypes.c_uint, ctypes.c_uint, vp]
+    lib.attn_bench_empty.restype = ctypes.c_int
     return lib
+
+
+def bench_launch_floor(torch, A, hipgraph, kernels, wgs, steps, warmup):
+    """ms per step of `kernels` dependent launches of an empty kernel (`wgs`
+    workgroups of 256 threads), timed like the short prompts: the fixed cost
+    a one- or two-kernel call pays in a graph before any work."""
+    sink = torch.zeros(wgs, dtype=torch.int32, device="cuda")
+    blib = bench_lib()
+
+    def launch(i, sp):
+        for _ in range(kernels):
+            assert blib.attn_bench_empty(sink.data_ptr(), wgs, 0, sp) == 0
+
+    return time_graph(torch, A, hipgraph, launch, steps, warmup, torch.cuda.Stream())[0]
 
 
 def bench_read_ceiling(torch, A, hipgraph, L, nbuf, steps, warmup, wgs=1024, seed=3):
@@ -719,6 +735,12 @@ def main():
         p254 = bench_prefill_graph(torch, A, hipgraph, 254, steps, warmup)
         detail["prefill"]["254"] = {"us": p254 * 1e3, "TFLOPs": prefill_flops(254) / p254 / 1e9}
         log(f"prefill N=254: {p254 * 1e3:.1f} us")
+        f1 = bench_launch_floor(torch, A, hipgraph, 1, 128, steps, warmup)
+        f2 = bench_launch_floor(torch, A, hipgraph, 2, 128, steps, warmup)
+        detail["launch_floor"] = {"one_kernel_us": f1 * 1e3, "two_kernels_us": f2 * 1e3,
+                                  "workgroups": 128}
+        log(f"launch floor (empty kernel, 128 workgroups, in a graph): one {f1 * 1e3:.2f} us, "
+            f"two dependent {f2 * 1e3:.2f} us")
         r8k = bench_rope(torch, A, hipgraph, 8192, 4, max(20, steps // 4), 5)
         r254 = bench_rope(torch, A, hipgraph, 254, 1, steps, warmup)
         r1 = bench_rope(torch, A, hipgraph, 1, 1, steps, warmup)

@@ -14,10 +14,11 @@
 //  * K and V of a 64-key tile are staged in LDS once per workgroup and shared
 //    by the 4 heads (the reference re-reads them per head), copied straight
 //    from global memory into LDS by buffer_load ... lds (no VGPRs, no LDS
-//    stores).  Rows are padded (K 272 B, V 320 B) so the MFMA operand reads
-//    are free of bank conflicts; a DMA instruction writes 1 KiB of LDS and
-//    the lanes that land on padding fetch a harmless copy of a row's first
-//    16 bytes.  Rows past N read as zero through the buffer range check.
+//    stores).  K rows are padded to 272 B and V rows are XOR-swizzled in
+//    16-byte chunks, so the MFMA operand reads are free of bank conflicts; a
+//    DMA instruction writes 1 KiB of LDS, and the K lanes that land on
+//    padding fetch a harmless copy of a row's first 16 bytes.  Rows past N
+//    read as zero through the buffer range check.
 //  * S^T = K . Q^T with v_mfma_f32_32x32x16_f16: keys are MFMA rows, queries
 //    columns, so each lane holds one query's scores and the online softmax
 //    (running max, running sum, rescale) is per lane plus one xor-32 exchange.
@@ -48,14 +49,23 @@ constexpr int kD = 128;
 constexpr int kBM = 64;        // query tokens per workgroup, at most
 constexpr int kBN = 64;        // keys per tile
 constexpr int kKP = kD + 8;    // K row pitch (halves): conflict-free 16 B A-operand reads
-// V row pitch (halves): 320-byte rows start 16 banks apart, so the 4 rows x
-// 64 bytes that 32 lanes of a transposing read address cover the 64 banks
-// once (288-byte rows overlapped by 8 banks: 2-way conflicts)
-constexpr int kVP = kD + 32;
+// V rows are unpadded (256 B) with their 16-byte chunks XOR-swizzled: chunk
+// c of row r sits at chunk c ^ 4 (r % 4).  The 32 lanes of half a transposing
+// read address 4 consecutive rows (r % 4 = 0..3) x 64 bytes of one 32-dim
+// tile; the swizzle puts those rows' 64 bytes in 4 different 64-byte bank
+// groups, so they cover the 64 banks once.  Against 320-byte padded rows it
+// copies 16 KiB per tile instead of 20 KiB.
+constexpr int kVP = kD;
 constexpr int kKChunks = kKP / 8;             // 16-byte LDS chunks per K row (17)
-constexpr int kVChunks = kVP / 8;             // ... per V row (20)
+constexpr int kVChunks = kVP / 8;             // ... per V row (16)
 constexpr int kKDma = kBN * kKChunks / 64;    // 1 KiB DMA instructions per K tile (17)
-constexpr int kVDma = kBN * kVChunks / 64;    // ... per V tile (20)
+constexpr int kVDma = kBN * kVChunks / 64;    // ... per V tile (16)
+constexpr int kMaxDma = kKDma > kVDma ? kKDma : kVDma;
+
+// LDS chunk position pos of V row r holds the row's 16-byte chunk pos ^ 4 (r % 4)
+__device__ __forceinline__ uint32_t v_src_chunk(uint32_t r, uint32_t pos) {
+    return pos ^ (4u * (r & 3u));
+}
 
 #define LDS_AS __attribute__((address_space(3)))
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -101,7 +111,7 @@ __device__ __forceinline__ bool map_block(uint32_t bid, uint32_t quads, uint32_t
 // fp16 and the O^T accumulators are rarely touched by VALU code.
 constexpr float kRescaleSlack = 8.0f;
 
-// Key tiles an ALL workgroup stages at once: 4 x (17,408 + 20,480) B of LDS
+// Key tiles an ALL workgroup stages at once: 4 x (17,408 + 16,384) B of LDS
 constexpr uint32_t kAllTiles = 4;
 
 // WAVES = 8: 64 queries of 4 heads per workgroup, two waves per SIMD (long
@@ -127,7 +137,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
     static_assert(!SK || ALL, "split keys needs every key tile staged at once");
     constexpr int kW = WAVES;
     constexpr int kBMw = 8 * WAVES;                     // query tokens per workgroup
-    constexpr int kDpw = (kVDma + WAVES - 1) / WAVES;   // DMA instructions per wave
+    constexpr int kDpw = (kMaxDma + WAVES - 1) / WAVES;   // DMA instructions per wave
     // two LDS buffers per operand as distinct objects, so the compiler can
     // tell a DMA into one buffer from the reads of the other (ALL: one buffer
     // per key tile, all filled before any is read)
@@ -191,7 +201,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         const uint32_t kr = q / kKChunks, kc = q % kKChunks;
         const uint32_t vr = q / kVChunks, vc = q % kVChunks;
         koff[t] = kr * kv_row_bytes + (kc < 16 ? kc : 0u) * 16u;
-        voff[t] = vr * kv_row_bytes + (vc < 16 ? vc : 0u) * 16u;
+        voff[t] = vr * kv_row_bytes + v_src_chunk(vr, vc) * 16u;
     }
     const f16* kbase = a.k + (uint64_t)g * kD;
     const f16* vbase = a.v + (uint64_t)g * kD;
@@ -224,9 +234,14 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
 
     // transposing-read address of lane (hh, n): group grp = lane / 16 holds
     // dims 16 (grp & 1) + 0..15 of a 32-dim tile; its lane j addresses key
-    // 4 hh + j / 4 (+ the k-step and half offsets), dims 4 (j & 3) + 0..3
+    // 4 hh + j / 4 (+ the k-step and half offsets, multiples of 8 keys, so
+    // the key's r % 4 is j / 4), dims 4 (j & 3) + 0..3, whose chunk of dim
+    // tile dt is swizzled to 4 (dt ^ (j / 4)) + 2 (grp & 1) + (j & 3) / 2
     const uint32_t grp = (uint32_t)lane >> 4, jl = (uint32_t)lane & 15u;
     const uint32_t vrd = (4u * hh + (jl >> 2)) * kVP + 16u * (grp & 1u) + 4u * (jl & 3u);
+    uint32_t vdt[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) vdt[dt] = vrd + 32u * ((uint32_t)dt ^ (jl >> 2));
 
     // one 64-key tile: S^T = K . Q^T, online softmax, O^T += V^T . P^T
     auto tile_step = [&](const f16* kt, const f16* vt, uint32_t j, auto diag_tag) {
@@ -282,15 +297,14 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         // P one 16-key MFMA step at a time, consumed at once by that step's
         // PV MFMAs: exps of step ks+1 overlap the MFMAs of step ks.  Step ks
         // covers keys 32 (ks / 2) + 16 (ks % 2) + 8 (e / 4) + 4 hh + e % 4.
-        const f16* vb = vt + vrd;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const int koffs = (32 * (ks >> 1) + 16 * (ks & 1)) * kVP;
             f16x8 va[4];
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const f16x4 lo = lds_tr4(vb + koffs + 32 * dt);
-                const f16x4 hi = lds_tr4(vb + koffs + 8 * kVP + 32 * dt);
+                const f16x4 lo = lds_tr4(vt + vdt[dt] + koffs);
+                const f16x4 hi = lds_tr4(vt + vdt[dt] + koffs + 8 * kVP);
                 va[dt] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             }
             f16x8 pb;
@@ -325,7 +339,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
             const BufRsrc rk = make_rsrc(kbase + (uint64_t)kv0 * a.kv_stride, bytes);
             const BufRsrc rv = make_rsrc(vbase + (uint64_t)kv0 * a.kv_stride, bytes);
 #pragma unroll
-            for (int i = 0; i < kVDma; ++i) {
+            for (int i = 0; i < kMaxDma; ++i) {
                 const uint32_t q = (uint32_t)i * 64u + (uint32_t)lane;
                 if (i < kKDma) {
                     const uint32_t kr = q / kKChunks, kc = q % kKChunks;
@@ -333,10 +347,12 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
                         rk, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)ktt + 1024 * i), 16,
                         (int)(kr * kv_row_bytes + (kc < 16 ? kc : 0u) * 16u), 0, 0, 0);
                 }
-                const uint32_t vr = q / kVChunks, vc = q % kVChunks;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rv, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)vtt + 1024 * i), 16,
-                    (int)(vr * kv_row_bytes + (vc < 16 ? vc : 0u) * 16u), 0, 0, 0);
+                if (i < kVDma) {
+                    const uint32_t vr = q / kVChunks, vc = q % kVChunks;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        rv, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)vtt + 1024 * i), 16,
+                        (int)(vr * kv_row_bytes + v_src_chunk(vr, vc) * 16u), 0, 0, 0);
+                }
             }
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             if (t < last)
@@ -351,13 +367,15 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
             // Every wave with a tile has a finite m_used: full tiles hold only
             // keys below the first query (and below N), and the diagonal tile
             // holds key 64 last <= every query of the tile.  The waves with a
-            // tile leave (O^T, m, l) in LDS over the K tiles; then wave w folds
-            // the 32 output dims 32 w .. 32 w + 31 of every state and stores
-            // them, so the epilogue's work is split four ways.
+            // tile leave (O^T, m, l) in LDS over their own K tile, which no
+            // other wave reads, so no barrier precedes the writes (C2 6.64 ->
+            // 6.53 us); then wave w folds the 32 output dims 32 w .. 32 w + 31
+            // of every state and stores them, so the epilogue's work is split
+            // four ways.  Keeping wave w's own words in registers instead of
+            // reading them back measured slower (6.7-6.8 us).
             // State of wave t in LDS, 16-byte words per lane: [t][17][64] x
-            // f32x4 = 17,408 B per wave (words 0-15: O^T of dims 32 dt + ...,
-            // word 16: (m, l))
-            __syncthreads();  // every wave has finished reading K and V
+            // f32x4 = 17,408 B per wave = one K tile (words 0-15: O^T of dims
+            // 32 dt + ..., word 16: (m, l))
             f32x4* st = reinterpret_cast<f32x4*>(kt0);  // [4][17][64] (69,632 B)
             if (t <= last) {
                 f32x4* w = st + t * (17u * 64u) + (uint32_t)lane;
@@ -456,8 +474,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
 // head's 32-query tile (queries 32 t .. 32 t + 31, keys 0 .. 32 t + 31); wave
 // w owns key unit w (keys 32 w .. 32 w + 31) if w <= t.  Each wave copies its
 // K unit (32 rows at pitch kKP: 9 DMA instructions, the last half of the
-// ninth re-fetching row 0 into padding) and V unit (32 rows at pitch kVP: 10
-// instructions) into its own 19 KiB LDS region, waits for its own copy, and
+// ninth re-fetching row 0 into padding) and V unit (32 swizzled rows: 8
+// instructions) into its own 17 KiB LDS region, waits for its own copy, and
 // computes S^T, the exact maximum of its 32 keys (one unit per wave, so no
 // running rescale), P and O^T.  Its state (O^T, m, l) then overwrites its own
 // region; after one barrier wave w folds output dims 32 (w / 2) + 8 i4 +
@@ -470,8 +488,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
 constexpr int kSkUnit = 32;                            // keys per wave
 constexpr int kSkWaves = 8;                            // units per query tile, at most
 constexpr int kSkKDma = 9;                             // 32 x 17 chunks = 8.5 KiB, rounded up
-constexpr int kSkVDma = kSkUnit * kVChunks / 64;       // 10
-constexpr int kSkRegion = (kSkKDma + kSkVDma) * 1024;  // 19,456 B per wave
+constexpr int kSkVDma = kSkUnit * kVChunks / 64;       // 8
+constexpr int kSkRegion = (kSkKDma + kSkVDma) * 1024;  // 17,408 B per wave
 constexpr uint32_t kSkMaxTokens = kSkWaves * kSkUnit;  // 256
 
 __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) {
@@ -521,7 +539,7 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
             const uint32_t vr = q / kVChunks, vc = q % kVChunks;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rv, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)region + 1024 * (kSkKDma + i)), 16,
-                (int)(vr * kv_row_bytes + (vc < 16 ? vc : 0u) * 16u), 0, 0, 0);
+                (int)(vr * kv_row_bytes + v_src_chunk(vr, vc) * 16u), 0, 0, 0);
         }
         // Q^T B operands (lane (hh, n): Q[q0 + n][head][16 s + 8 hh .. +7]),
         // loaded while the copy is in flight; rows past N read as zero
@@ -561,14 +579,17 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
         const float mneg = -m_unit;
         const uint32_t grp = (uint32_t)lane >> 4, jl = (uint32_t)lane & 15u;
         const f16* vb = vt + (4u * hh + (jl >> 2)) * kVP + 16u * (grp & 1u) + 4u * (jl & 3u);
+        uint32_t vdt[4];
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) vdt[dt] = 32u * ((uint32_t)dt ^ (jl >> 2));
         float psum = 0.f;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             f16x8 va[4];
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const f16x4 lo = lds_tr4(vb + 16 * ks * kVP + 32 * dt);
-                const f16x4 hi = lds_tr4(vb + (16 * ks + 8) * kVP + 32 * dt);
+                const f16x4 lo = lds_tr4(vb + vdt[dt] + 16 * ks * kVP);
+                const f16x4 hi = lds_tr4(vb + vdt[dt] + (16 * ks + 8) * kVP);
                 va[dt] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             }
             f16x8 pb;
