@@ -62,6 +62,11 @@ constexpr int kKDma = kBN * kKChunks / 64;    // 1 KiB DMA instructions per K ti
 constexpr int kVDma = kBN * kVChunks / 64;    // ... per V tile (16)
 constexpr int kMaxDma = kKDma > kVDma ? kKDma : kVDma;
 
+// s_waitcnt immediate that waits until at most n vector-memory loads are
+// outstanding (vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt not waited on)
+constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 0xF) | ((n >> 4) << 14); }
+static_assert(vmcnt_imm(0) == 0x0F70 && vmcnt_imm(16) == 0x4F70 && vmcnt_imm(63) == 0xCF7F);
+
 // LDS chunk position pos of V row r holds the row's 16-byte chunk pos ^ 4 (r % 4)
 __device__ __forceinline__ uint32_t v_src_chunk(uint32_t r, uint32_t pos) {
     return pos ^ (4u * (r & 3u));
@@ -244,8 +249,12 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
     for (int dt = 0; dt < 4; ++dt) vdt[dt] = vrd + 32u * ((uint32_t)dt ^ (jl >> 2));
 
     // one 64-key tile: S^T = K . Q^T, online softmax, O^T += V^T . P^T
-    auto tile_step = [&](const f16* kt, const f16* vt, uint32_t j, auto diag_tag) {
+    // kVWait: the caller's V copy may still be in flight (split keys: the K
+    // copy was issued first and awaited alone), so wait for it before PV
+    auto tile_step = [&](const f16* kt, const f16* vt, uint32_t j, auto diag_tag,
+                         auto v_wait_tag) {
         constexpr bool kDiag = decltype(diag_tag)::value;
+        constexpr bool kVWait = decltype(v_wait_tag)::value;
         // the compiler's interleaving strategy for LDS reads and MFMAs
         // (iglp_opt 0): 8-wave tile at C4 261.7 against 265.8 us (median of
         // six 100-launch medians each, same box), identical bits
@@ -294,9 +303,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         }
         const float mneg = -m_used;
         float psum = 0.f;
+
         // P one 16-key MFMA step at a time, consumed at once by that step's
         // PV MFMAs: exps of step ks+1 overlap the MFMAs of step ks.  Step ks
         // covers keys 32 (ks / 2) + 16 (ks % 2) + 8 (e / 4) + 4 hh + e % 4.
+        if constexpr (kVWait) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const int koffs = (32 * (ks >> 1) + 16 * (ks & 1)) * kVP;
@@ -339,26 +350,28 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
             const BufRsrc rk = make_rsrc(kbase + (uint64_t)kv0 * a.kv_stride, bytes);
             const BufRsrc rv = make_rsrc(vbase + (uint64_t)kv0 * a.kv_stride, bytes);
 #pragma unroll
-            for (int i = 0; i < kMaxDma; ++i) {
+            for (int i = 0; i < kKDma; ++i) {
                 const uint32_t q = (uint32_t)i * 64u + (uint32_t)lane;
-                if (i < kKDma) {
-                    const uint32_t kr = q / kKChunks, kc = q % kKChunks;
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        rk, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)ktt + 1024 * i), 16,
-                        (int)(kr * kv_row_bytes + (kc < 16 ? kc : 0u) * 16u), 0, 0, 0);
-                }
-                if (i < kVDma) {
-                    const uint32_t vr = q / kVChunks, vc = q % kVChunks;
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        rv, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)vtt + 1024 * i), 16,
-                        (int)(vr * kv_row_bytes + v_src_chunk(vr, vc) * 16u), 0, 0, 0);
-                }
+                const uint32_t kr = q / kKChunks, kc = q % kKChunks;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rk, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)ktt + 1024 * i), 16,
+                    (int)(kr * kv_row_bytes + (kc < 16 ? kc : 0u) * 16u), 0, 0, 0);
             }
-            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+#pragma unroll
+            for (int i = 0; i < kVDma; ++i) {
+                const uint32_t q = (uint32_t)i * 64u + (uint32_t)lane;
+                const uint32_t vr = q / kVChunks, vc = q % kVChunks;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rv, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)vtt + 1024 * i), 16,
+                    (int)(vr * kv_row_bytes + v_src_chunk(vr, vc) * 16u), 0, 0, 0);
+            }
+            // Q and K have landed once at most the kVDma V copies are
+            // outstanding (loads complete in order); V is awaited before PV
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(kVDma));
             if (t < last)
-                tile_step(ktt, vtt, t, std::false_type{});
+                tile_step(ktt, vtt, t, std::false_type{}, std::true_type{});
             else
-                tile_step(ktt, vtt, t, std::true_type{});
+                tile_step(ktt, vtt, t, std::true_type{}, std::true_type{});
         }
         if (last == 0) {
             // one tile: wave 0 holds the whole state and finishes below
@@ -424,8 +437,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         {
 #pragma unroll 1
             for (uint32_t t = 0; t < last; ++t)
-                tile_step(kt0 + t * (kBN * kKP), vt0 + t * (kBN * kVP), t, std::false_type{});
-            tile_step(kt0 + last * (kBN * kKP), vt0 + last * (kBN * kVP), last, std::true_type{});
+                tile_step(kt0 + t * (kBN * kKP), vt0 + t * (kBN * kVP), t, std::false_type{}, std::false_type{});
+            tile_step(kt0 + last * (kBN * kKP), vt0 + last * (kBN * kVP), last, std::true_type{}, std::false_type{});
         }
     } else {
     // Tile t sits in buffer t & 1.  Full tiles 0..last-1 need no mask; tile
@@ -436,19 +449,19 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
     uint32_t j = 0;
     for (; j + 2 <= last; j += 2) {
         stage((j + 1) * kBN, kt1, vt1);
-        tile_step(kt0, vt0, j, std::false_type{});
+        tile_step(kt0, vt0, j, std::false_type{}, std::false_type{});
         publish();
         stage((j + 2) * kBN, kt0, vt0);
-        tile_step(kt1, vt1, j + 1, std::false_type{});
+        tile_step(kt1, vt1, j + 1, std::false_type{}, std::false_type{});
         publish();
     }
     if (j < last) {  // j even: tile j in buffer 0, the diagonal tile j + 1 in buffer 1
         stage((j + 1) * kBN, kt1, vt1);
-        tile_step(kt0, vt0, j, std::false_type{});
+        tile_step(kt0, vt0, j, std::false_type{}, std::false_type{});
         publish();
-        tile_step(kt1, vt1, last, std::true_type{});
+        tile_step(kt1, vt1, last, std::true_type{}, std::false_type{});
     } else {
-        tile_step(kt0, vt0, last, std::true_type{});
+        tile_step(kt0, vt0, last, std::true_type{}, std::false_type{});
     }
     }
 
@@ -533,6 +546,15 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
                 rk, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)region + 1024 * i), 16, (int)off, 0,
                 0, 0);
         }
+        // Q^T B operands (lane (hh, n): Q[q0 + n][head][16 s + 8 hh .. +7]),
+        // loaded between the K and the V copies; rows past N read as zero
+        const uint32_t q_row_bytes = (uint32_t)(a.q_stride * 2);
+        const BufRsrc rq = make_rsrc(a.q + (uint64_t)head * kD,
+                                     __builtin_amdgcn_readfirstlane((N - 1) * q_row_bytes + kD * 2));
+        f16x8 qb[8];
+        const uint32_t qoff = (q0 + n) * q_row_bytes + 16u * hh;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) qb[s] = buf_ld16(rq, qoff + 32u * s);
 #pragma unroll
         for (int i = 0; i < kSkVDma; ++i) {
             const uint32_t q = (uint32_t)i * 64u + (uint32_t)lane;
@@ -541,17 +563,10 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
                 rv, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)region + 1024 * (kSkKDma + i)), 16,
                 (int)(vr * kv_row_bytes + v_src_chunk(vr, vc) * 16u), 0, 0, 0);
         }
-        // Q^T B operands (lane (hh, n): Q[q0 + n][head][16 s + 8 hh .. +7]),
-        // loaded while the copy is in flight; rows past N read as zero
-        const uint32_t q_row_bytes = (uint32_t)(a.q_stride * 2);
-        const BufRsrc rq = make_rsrc(a.q + (uint64_t)head * kD,
-                                     __builtin_amdgcn_readfirstlane((N - 1) * q_row_bytes + kD * 2));
-        f16x8 qb[8];
-        const uint32_t qoff = (q0 + n) * q_row_bytes + 16u * hh;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) qb[s] = buf_ld16(rq, qoff + 32u * s);
-        // a wave sees its own LDS-DMA writes once vmcnt reaches 0
-        __builtin_amdgcn_s_waitcnt(0x0F70);
+        // a wave sees its own LDS-DMA writes once they are no longer counted
+        // in vmcnt (loads complete in order): K and Q have landed once at
+        // most the kSkVDma V copies are outstanding; V is awaited before PV
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kSkVDma));
 
         const f16* kt = reinterpret_cast<const f16*>(region);
         const f16* vt = reinterpret_cast<const f16*>(region + kSkKDma * 1024);
@@ -583,6 +598,7 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) vdt[dt] = 32u * ((uint32_t)dt ^ (jl >> 2));
         float psum = 0.f;
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             f16x8 va[4];
