@@ -38,7 +38,6 @@ constexpr int kRound = 4;  // splits per wave per round of loads
 constexpr uint32_t kXcds = 8;
 constexpr int kSc1 = 16;  // cache-policy bit sc1 of buffer loads: device-coherent
 
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float ldf(BufRsrc r, uint32_t byte_off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 0));

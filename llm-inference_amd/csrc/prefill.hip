@@ -14,11 +14,10 @@
 //  * K and V of a 64-key tile are staged in LDS once per workgroup and shared
 //    by the 4 heads (the reference re-reads them per head), copied straight
 //    from global memory into LDS by buffer_load ... lds (no VGPRs, no LDS
-//    stores).  K rows are padded to 272 B and V rows are XOR-swizzled in
-//    16-byte chunks, so the MFMA operand reads are free of bank conflicts; a
-//    DMA instruction writes 1 KiB of LDS, and the K lanes that land on
-//    padding fetch a harmless copy of a row's first 16 bytes.  Rows past N
-//    read as zero through the buffer range check.
+//    stores).  K and V rows are unpadded with their 16-byte chunks
+//    XOR-swizzled by row, so the MFMA operand reads are free of bank
+//    conflicts; a DMA instruction writes 1 KiB of LDS (4 key rows).  Rows
+//    past N read as zero through the buffer range check.
 //  * S^T = K . Q^T with v_mfma_f32_32x32x16_f16: keys are MFMA rows, queries
 //    columns, so each lane holds one query's scores and the online softmax
 //    (running max, running sum, rescale) is per lane plus one xor-32 exchange.
@@ -48,7 +47,14 @@ namespace {
 constexpr int kD = 128;
 constexpr int kBM = 64;        // query tokens per workgroup, at most
 constexpr int kBN = 64;        // keys per tile
-constexpr int kKP = kD + 8;    // K row pitch (halves): conflict-free 16 B A-operand reads
+// K rows are unpadded (256 B) with their 16-byte chunks XOR-swizzled: chunk
+// c of row r sits at chunk c ^ (r % 16).  The 16 lanes of one phase of an
+// A-operand read (ds_read_b128) address 16 consecutive rows at the same
+// chunk, which the swizzle spreads over 16 chunks = the 64 banks; each lane
+// keeps one address per k-step (8 VGPRs), so the tile loop gains no
+// instruction.  Against 272-byte padded rows it copies 16 KiB per tile
+// instead of 17 KiB.
+constexpr int kKP = kD;
 // V rows are unpadded (256 B) with their 16-byte chunks XOR-swizzled: chunk
 // c of row r sits at chunk c ^ 4 (r % 4).  The 32 lanes of half a transposing
 // read address 4 consecutive rows (r % 4 = 0..3) x 64 bytes of one 32-dim
@@ -56,9 +62,9 @@ constexpr int kKP = kD + 8;    // K row pitch (halves): conflict-free 16 B A-ope
 // groups, so they cover the 64 banks once.  Against 320-byte padded rows it
 // copies 16 KiB per tile instead of 20 KiB.
 constexpr int kVP = kD;
-constexpr int kKChunks = kKP / 8;             // 16-byte LDS chunks per K row (17)
+constexpr int kKChunks = kKP / 8;             // 16-byte LDS chunks per K row (16)
 constexpr int kVChunks = kVP / 8;             // ... per V row (16)
-constexpr int kKDma = kBN * kKChunks / 64;    // 1 KiB DMA instructions per K tile (17)
+constexpr int kKDma = kBN * kKChunks / 64;    // 1 KiB DMA instructions per K tile (16)
 constexpr int kVDma = kBN * kVChunks / 64;    // ... per V tile (16)
 constexpr int kMaxDma = kKDma > kVDma ? kKDma : kVDma;
 
@@ -66,6 +72,17 @@ constexpr int kMaxDma = kKDma > kVDma ? kKDma : kVDma;
 // outstanding (vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt not waited on)
 constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 0xF) | ((n >> 4) << 14); }
 static_assert(vmcnt_imm(0) == 0x0F70 && vmcnt_imm(16) == 0x4F70 && vmcnt_imm(63) == 0xCF7F);
+
+// LDS chunk position pos of K row r holds the row's 16-byte chunk pos ^ (r % 16)
+__device__ __forceinline__ uint32_t k_src_chunk(uint32_t r, uint32_t pos) {
+    return pos ^ (r & 15u);
+}
+
+// LDS offset (halves) of lane (hh, n)'s A operand at k-step ks: row n, the
+// 16-byte chunk 2 ks + hh, swizzled
+__device__ __forceinline__ uint32_t k_read_offset(uint32_t n, uint32_t hh, uint32_t ks) {
+    return n * kKP + 8u * k_src_chunk(n, 2u * ks + hh);
+}
 
 // LDS chunk position pos of V row r holds the row's 16-byte chunk pos ^ 4 (r % 4)
 __device__ __forceinline__ uint32_t v_src_chunk(uint32_t r, uint32_t pos) {
@@ -116,7 +133,7 @@ __device__ __forceinline__ bool map_block(uint32_t bid, uint32_t quads, uint32_t
 // fp16 and the O^T accumulators are rarely touched by VALU code.
 constexpr float kRescaleSlack = 8.0f;
 
-// Key tiles an ALL workgroup stages at once: 4 x (17,408 + 16,384) B of LDS
+// Key tiles an ALL workgroup stages at once: 4 x (16,384 + 16,384) B of LDS
 constexpr uint32_t kAllTiles = 4;
 
 // WAVES = 8: 64 queries of 4 heads per workgroup, two waves per SIMD (long
@@ -152,6 +169,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) f16 kt1[ALL ? 8 : kBN * kKP];
     __shared__ __attribute__((aligned(16))) f16 vt0[kVBuf];
     __shared__ __attribute__((aligned(16))) f16 vt1[ALL ? 8 : kBN * kVP];
+    // split keys: each wave's (m, l) for the combine
+    __shared__ f32x2 sml[SK ? kAllTiles : 1][64];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -205,7 +224,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         const uint32_t q = (uint32_t)(wave + kW * t) * 64u + (uint32_t)lane;
         const uint32_t kr = q / kKChunks, kc = q % kKChunks;
         const uint32_t vr = q / kVChunks, vc = q % kVChunks;
-        koff[t] = kr * kv_row_bytes + (kc < 16 ? kc : 0u) * 16u;
+        koff[t] = kr * kv_row_bytes + k_src_chunk(kr, kc) * 16u;
         voff[t] = vr * kv_row_bytes + v_src_chunk(vr, vc) * 16u;
     }
     const f16* kbase = a.k + (uint64_t)g * kD;
@@ -247,6 +266,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
     uint32_t vdt[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) vdt[dt] = vrd + 32u * ((uint32_t)dt ^ (jl >> 2));
+    uint32_t kofs[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) kofs[ks] = k_read_offset(n, hh, ks);
 
     // one 64-key tile: S^T = K . Q^T, online softmax, O^T += V^T . P^T
     // kVWait: the caller's V copy may still be in flight (split keys: the K
@@ -260,17 +282,17 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         // six 100-launch medians each, same box), identical bits
         if constexpr (WAVES == 8) __builtin_amdgcn_iglp_opt(0);
         f32x16 s[2] = {f32x16{}, f32x16{}};
-        // K operands are read one k-step ahead of their MFMAs
-        const f16* kb = kt + n * kKP + 8 * hh;
+        // K operands are read one k-step ahead of their MFMAs (rows n and
+        // n + 32 share the swizzle)
         f16x8 ka[2][2];
-        ka[0][0] = lds16(kb);
-        ka[0][1] = lds16(kb + 32 * kKP);
+        ka[0][0] = lds16(kt + kofs[0]);
+        ka[0][1] = lds16(kt + kofs[0] + 32 * kKP);
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             const int cur = ks & 1;
             if (ks + 1 < 8) {
-                ka[cur ^ 1][0] = lds16(kb + 16 * (ks + 1));
-                ka[cur ^ 1][1] = lds16(kb + 32 * kKP + 16 * (ks + 1));
+                ka[cur ^ 1][0] = lds16(kt + kofs[ks + 1]);
+                ka[cur ^ 1][1] = lds16(kt + kofs[ks + 1] + 32 * kKP);
             }
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) s[mt] = mfma32(ka[cur][mt], qb[ks], s[mt]);
@@ -355,7 +377,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
                 const uint32_t kr = q / kKChunks, kc = q % kKChunks;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     rk, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)ktt + 1024 * i), 16,
-                    (int)(kr * kv_row_bytes + (kc < 16 ? kc : 0u) * 16u), 0, 0, 0);
+                    (int)(kr * kv_row_bytes + k_src_chunk(kr, kc) * 16u), 0, 0, 0);
             }
 #pragma unroll
             for (int i = 0; i < kVDma; ++i) {
@@ -386,25 +408,25 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
             // of every state and stores them, so the epilogue's work is split
             // four ways.  Keeping wave w's own words in registers instead of
             // reading them back measured slower (6.7-6.8 us).
-            // State of wave t in LDS, 16-byte words per lane: [t][17][64] x
-            // f32x4 = 17,408 B per wave = one K tile (words 0-15: O^T of dims
-            // 32 dt + ..., word 16: (m, l))
-            f32x4* st = reinterpret_cast<f32x4*>(kt0);  // [4][17][64] (69,632 B)
+            // State of wave t in LDS, 16-byte words per lane: [t][16][64] x
+            // f32x4 = 16,384 B per wave = one K tile (word e: O^T dims of
+            // o[e / 4][4 (e % 4) .. +3]), and (m, l) in sml[t][lane]
+            f32x4* st = reinterpret_cast<f32x4*>(kt0);  // [4][16][64] (65,536 B)
             if (t <= last) {
-                f32x4* w = st + t * (17u * 64u) + (uint32_t)lane;
+                f32x4* w = st + t * (16u * 64u) + (uint32_t)lane;
 #pragma unroll
                 for (int e = 0; e < 16; ++e)
                     w[64 * e] = f32x4{o[e >> 2][4 * (e & 3)], o[e >> 2][4 * (e & 3) + 1],
                                       o[e >> 2][4 * (e & 3) + 2], o[e >> 2][4 * (e & 3) + 3]};
-                w[64 * 16] = f32x4{m_used, l_run, 0.f, 0.f};
+                sml[t][lane] = f32x2{m_used, l_run};
             }
             __syncthreads();
             const int dt = wave;
             float m = -INFINITY, l = 0.f;
             f32x16 acc = f32x16{};
             for (uint32_t w2 = 0; w2 <= last; ++w2) {
-                const f32x4* w = st + w2 * (17u * 64u) + (uint32_t)lane;
-                const f32x4 ml = w[64 * 16];
+                const f32x4* w = st + w2 * (16u * 64u) + (uint32_t)lane;
+                const f32x2 ml = sml[w2][lane];
                 f32x4 ow[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) ow[q] = w[64 * (4 * dt + q)];
@@ -486,12 +508,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
 // Split keys over 8 waves of 32 keys each (N <= 256).  A workgroup is ONE
 // head's 32-query tile (queries 32 t .. 32 t + 31, keys 0 .. 32 t + 31); wave
 // w owns key unit w (keys 32 w .. 32 w + 31) if w <= t.  Each wave copies its
-// K unit (32 rows at pitch kKP: 9 DMA instructions, the last half of the
-// ninth re-fetching row 0 into padding) and V unit (32 swizzled rows: 8
-// instructions) into its own 17 KiB LDS region, waits for its own copy, and
+// K unit and V unit (32 swizzled rows each: 8 DMA instructions each) into its
+// own 16 KiB LDS region, waits for its own copy, and
 // computes S^T, the exact maximum of its 32 keys (one unit per wave, so no
-// running rescale), P and O^T.  Its state (O^T, m, l) then overwrites its own
-// region; after one barrier wave w folds output dims 32 (w / 2) + 8 i4 +
+// running rescale), P and O^T.  Its state (O^T) then overwrites its own
+// region and (m, l) goes to a small array; after one barrier wave w folds output dims 32 (w / 2) + 8 i4 +
 // 4 hh + 0..3 for i4 = 2 (w % 2), 2 (w % 2) + 1 over the states
 // (M = max m, l and O scaled by 2^(m - M) and added) and stores them.
 // Against the 4-wave form (one 64-key tile per wave): half the copy and half
@@ -500,13 +521,14 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
 // and read back through LDS).
 constexpr int kSkUnit = 32;                            // keys per wave
 constexpr int kSkWaves = 8;                            // units per query tile, at most
-constexpr int kSkKDma = 9;                             // 32 x 17 chunks = 8.5 KiB, rounded up
+constexpr int kSkKDma = kSkUnit * kKChunks / 64;       // 8
 constexpr int kSkVDma = kSkUnit * kVChunks / 64;       // 8
-constexpr int kSkRegion = (kSkKDma + kSkVDma) * 1024;  // 17,408 B per wave
+constexpr int kSkRegion = (kSkKDma + kSkVDma) * 1024;  // 16,384 B per wave
 constexpr uint32_t kSkMaxTokens = kSkWaves * kSkUnit;  // 256
 
 __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) char lds[kSkWaves * kSkRegion];
+    __shared__ f32x2 sml[kSkWaves][64];  // each unit's (m, l)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -539,12 +561,9 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
         for (int i = 0; i < kSkKDma; ++i) {
             const uint32_t q = (uint32_t)i * 64u + (uint32_t)lane;
             const uint32_t kr = q / kKChunks, kc = q % kKChunks;
-            const uint32_t off = q < (uint32_t)(kSkUnit * kKChunks)
-                                     ? kr * kv_row_bytes + (kc < 16 ? kc : 0u) * 16u
-                                     : 0u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rk, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)region + 1024 * i), 16, (int)off, 0,
-                0, 0);
+                rk, (LDS_AS void*)((LDS_AS char*)(LDS_AS void*)region + 1024 * i), 16,
+                (int)(kr * kv_row_bytes + k_src_chunk(kr, kc) * 16u), 0, 0, 0);
         }
         // Q^T B operands (lane (hh, n): Q[q0 + n][head][16 s + 8 hh .. +7]),
         // loaded between the K and the V copies; rows past N read as zero
@@ -573,9 +592,9 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
         // S^T = K . Q^T: lane (hh, n) holds keys 8 (i / 4) + 4 hh + i % 4 of
         // the unit for query n
         f32x16 s = f32x16{};
-        const f16* kb = kt + n * kKP + 8 * hh;
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) s = mfma32(lds16(kb + 16 * ks), qb[ks], s);
+        for (int ks = 0; ks < 8; ++ks)
+            s = mfma32(lds16(kt + k_read_offset((uint32_t)n, (uint32_t)hh, (uint32_t)ks)), qb[ks], s);
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -640,15 +659,16 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
         return;
     }
     // state of unit u over its own region, 16-byte words per lane: words
-    // 0-15 O^T (word e = o[e / 4][4 (e % 4) .. +3]), word 16 (m, l); the
-    // wave's own LDS reads of the region precede these writes in order
+    // 0-15 O^T (word e = o[e / 4][4 (e % 4) .. +3]), and (m, l) in
+    // sml[u][lane]; the wave's own LDS reads of the region precede these
+    // writes in order
     if (u <= last) {
         f32x4* w = reinterpret_cast<f32x4*>(region) + lane;
 #pragma unroll
         for (int e = 0; e < 16; ++e)
             w[64 * e] = f32x4{o[e >> 2][4 * (e & 3)], o[e >> 2][4 * (e & 3) + 1],
                               o[e >> 2][4 * (e & 3) + 2], o[e >> 2][4 * (e & 3) + 3]};
-        w[64 * 16] = f32x4{m_unit, l_unit, 0.f, 0.f};
+        sml[u][lane] = f32x2{m_unit, l_unit};
     }
     __syncthreads();
     const int dt = wave >> 1;
@@ -657,7 +677,7 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
     f32x4 acc[2] = {f32x4{}, f32x4{}};
     for (uint32_t w2 = 0; w2 <= last; ++w2) {
         const f32x4* w = reinterpret_cast<const f32x4*>(lds + w2 * kSkRegion) + lane;
-        const f32x4 ml = w[64 * 16];
+        const f32x2 ml = sml[w2][lane];
         const f32x4 o0 = w[64 * e0], o1 = w[64 * (e0 + 1)];
         const float mx = fmaxf(m, ml[0]);  // ml[0] is finite
         const float a1 = fast_exp2(m - mx), a2 = fast_exp2(ml[0] - mx);
