@@ -81,31 +81,6 @@ __device__ __forceinline__ f32x4 buf_ldf4(BufRsrc r, uint32_t byte_off) {
 // from moving stores across
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Combining a lane with lane ^ 16 or lane ^ 32 on the VALU (gfx950
-// v_permlane16_swap / v_permlane32_swap with both operands x: the first
-// result holds the even rows / lower half in both places, the second the
-// odd rows / upper half), in the same order in both lanes.
-__device__ __forceinline__ float sum_xor16(float x) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x),
-                                                    __builtin_bit_cast(unsigned, x), false, false);
-    return __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
-}
-__device__ __forceinline__ float sum_xor32(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
-                                                    __builtin_bit_cast(unsigned, x), false, false);
-    return __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
-}
-__device__ __forceinline__ float max_xor16(float x) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x),
-                                                    __builtin_bit_cast(unsigned, x), false, false);
-    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
-}
-__device__ __forceinline__ float max_xor32(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
-                                                    __builtin_bit_cast(unsigned, x), false, false);
-    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
-}
-
 // Reductions over the 64 lanes of a wave with a uniform result, for a wave
 // whose cross-lane steps sit on its critical path: two DPP quad permutes
 // (xor 1, xor 2) and two DPP row rotations (by 4 and 8 lanes) reduce each
