@@ -81,41 +81,6 @@ __device__ __forceinline__ f32x4 buf_ldf4(BufRsrc r, uint32_t byte_off) {
 // from moving stores across
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Reductions over the 64 lanes of a wave with a uniform result, for a wave
-// whose cross-lane steps sit on its critical path: two DPP quad permutes
-// (xor 1, xor 2) and two DPP row rotations (by 4 and 8 lanes) reduce each
-// 16-lane row into its every lane, then the four rows' lane-0 values are
-// read into scalars and combined as (r0 op r1) op (r2 op r3).  Each step
-// is a VALU instruction (a few cycles) where an xor shuffle is an LDS-unit
-// permute (~100 cycles of latency).  The result is the same in every lane
-// and does not depend on the lane's position.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-        0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float lane_f(float x, int l) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
-}
-constexpr int kDppXor1 = 0xB1;   // quad_perm [1, 0, 3, 2]
-constexpr int kDppXor2 = 0x4E;   // quad_perm [2, 3, 0, 1]
-constexpr int kDppRor4 = 0x124;  // row_ror:4
-constexpr int kDppRor8 = 0x128;  // row_ror:8
-__device__ __forceinline__ float wave_max(float x) {
-    x = fmaxf(x, dpp_f<kDppXor1>(x));
-    x = fmaxf(x, dpp_f<kDppXor2>(x));
-    x = fmaxf(x, dpp_f<kDppRor4>(x));
-    x = fmaxf(x, dpp_f<kDppRor8>(x));
-    return fmaxf(fmaxf(lane_f(x, 0), lane_f(x, 16)), fmaxf(lane_f(x, 32), lane_f(x, 48)));
-}
-__device__ __forceinline__ float wave_sum(float x) {
-    x += dpp_f<kDppXor1>(x);
-    x += dpp_f<kDppXor2>(x);
-    x += dpp_f<kDppRor4>(x);
-    x += dpp_f<kDppRor8>(x);
-    return (lane_f(x, 0) + lane_f(x, 16)) + (lane_f(x, 32) + lane_f(x, 48));
-}
-
 // The split kernel: grid (nsplit, Hkv / HPW); workgroup (c, grp) owns chunk c
 // of KV heads HPW*grp .. HPW*grp + HPW-1.  Wave w serves KV head
 // HPW*grp + w % HPW and every (8/HPW)-th batch of the chunk, so the waves of a

@@ -83,11 +83,10 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void qkv_gemv(QkvArgs a) {
             acc1 += (float)w1[c] * xc;
         }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        acc0 += xor_lane(acc0, o);
-        acc1 += xor_lane(acc1, o);
-    }
+    // wave sums on the VALU (DPP + lane reads): the reduction is the tail of
+    // every row pair's critical path
+    acc0 = wave_sum(acc0);
+    acc1 = wave_sum(acc1);
     if (lane != 0) return;
     if (!FUSED) {
         // matrix_vec_mul.hip.cpp:156-163: the fp32 sum plus beta * y, rounded once
