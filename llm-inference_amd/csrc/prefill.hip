@@ -32,10 +32,11 @@
 //    KV head's K/V stays in one L2.
 //  * Tile j+1 is copied into the other LDS buffer while tile j is computed;
 //    one barrier per tile.
-//  * Short prompts (N <= 256) split each 32-query tile's keys over the waves
+//  * Short prompts (N <= 1536) split each 32-query tile's keys over the waves
 //    of one head's workgroup and combine the partial states through LDS
-//    (prefill_d128<4, true, true>: 64-key tiles over 4 waves; prefill_sk32:
-//    32-key units over 8 waves, up to 32 tokens).
+//    (prefill_d128<4, true, true>: 64-key tiles over 4 waves, up to 256
+//    tokens; prefill_sk32: 32-key units over 8 waves, up to 32 tokens;
+//    prefill_skn: 32-key units streamed per wave, from 257 to 1536 tokens).
 #include "attn_internal.hpp"
 
 #include <type_traits>
@@ -703,6 +704,227 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
     }
 }
 
+// Split keys over 4 waves for prompts longer than the all-tiles-staged forms
+// take.  A workgroup is ONE head's 32-query tile t (keys 0 .. 32 t + 31 in
+// 32-key units 0 .. t); wave w owns units w, w + 4, w + 8, ... and streams
+// them through two 16 KiB LDS buffers of its own (K and V swizzled as above):
+// the copy of its unit k + 2 goes out once unit k is computed, and it waits
+// for its own copies only (vmcnt), so the waves run without barriers until
+// the combine.  Each wave keeps an online softmax with the lazy rescale of
+// the long-prompt kernel; at the end the states meet in LDS as in the other
+// split-keys forms (wave w folds output dims 32 w .. 32 w + 31).  Against
+// the 4-head workgroups of prefill_d128<4, false, false>: four times the
+// workgroups and a quarter of each one's chain, at four times the K/V reads
+// (one head per workgroup instead of 4).
+constexpr int kSknWaves = 4;
+// automatic up to this many tokens: from 257 tokens (beyond the all-tiles
+// forms) it measured 25-35 % faster than the 4-head workgroups (288 tokens
+// 7.3 against 10.4 us, 1024 tokens 17.9 against 23.4 us), level at 1536
+// (32.0 against 32.4 us) and slower from 1664 (37.0 against 34.6 us), where
+// the 4x K/V reads of one-head workgroups outweigh their parallelism
+constexpr uint32_t kSknMaxTokens = 1536;
+constexpr int kSknUnitBytes = 2 * kSkUnit * kD * 2;       // K + V of 32 keys: 16 KiB
+constexpr int kSknDma = kSknUnitBytes / 1024;             // 16: 8 for K, then 8 for V
+
+__global__ __launch_bounds__(64 * kSknWaves, 1) void prefill_skn(PrefillArgs a) {
+    // per wave two unit buffers: [wave][2][16 KiB]
+    __shared__ __attribute__((aligned(16))) char ub[kSknWaves * 2 * kSknUnitBytes];
+    __shared__ f32x2 sml[kSknWaves][64];  // each wave's (m, l)
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 31;
+    const int hh = lane >> 5;
+    uint32_t head, tile;
+    if (!map_block(blockIdx.x, a.num_heads, a.q_tiles, head, tile)) return;
+    const uint32_t last = tile;  // the diagonal unit
+    if (last == 0 && wave != 0) return;  // one unit: wave 0 finishes it alone
+    const uint32_t g = head / a.group;
+    const uint32_t q0 = tile * (uint32_t)kSkUnit;
+    const uint32_t N = a.seq_len;
+    const uint32_t kv_row_bytes = (uint32_t)(a.kv_stride * 2);
+    // units of this wave: wave, wave + 4, ... <= last
+    const uint32_t nunits = (uint32_t)wave <= last ? (last - (uint32_t)wave) / kSknWaves + 1u : 0u;
+    char* const mine = ub + wave * 2 * kSknUnitBytes;
+    const uint32_t mine_lds = lds_addr(mine);
+
+    f32x16 o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
+    float m_used = -INFINITY, l_run = 0.f;
+
+    // per-lane source offsets of the 16 copy instructions of a unit (K rows
+    // 4 i + lane / 16 for i < 8, then V rows): the same for every unit
+    uint32_t koff[kSknDma / 2], voff[kSknDma / 2];
+#pragma unroll
+    for (int i = 0; i < kSknDma / 2; ++i) {
+        const uint32_t q = (uint32_t)i * 64u + (uint32_t)lane;
+        const uint32_t r = q / kKChunks, c = q % kKChunks;
+        koff[i] = r * kv_row_bytes + k_src_chunk(r, c) * 16u;
+        voff[i] = r * kv_row_bytes + v_src_chunk(r, c) * 16u;
+    }
+    // copy unit u into buffer `buf` (K, then V); issued as inline assembly,
+    // so the only waits for it are the explicit vmcnt waits below
+    auto issue = [&](uint32_t u, uint32_t buf) {
+        const uint32_t kv0 = u * (uint32_t)kSkUnit;  // < N: u <= last and q0 < N
+        const uint32_t bytes = (N - kv0 - 1u) * kv_row_bytes + kD * 2;
+        const u32x4 rk = rsrc_words(a.k + (uint64_t)kv0 * a.kv_stride + (uint64_t)g * kD, bytes);
+        const u32x4 rv = rsrc_words(a.v + (uint64_t)kv0 * a.kv_stride + (uint64_t)g * kD, bytes);
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(mine_lds + buf * kSknUnitBytes);
+#pragma unroll
+        for (int i = 0; i < kSknDma / 2; ++i) dma16(rk, dst + 1024u * i, koff[i]);
+#pragma unroll
+        for (int i = 0; i < kSknDma / 2; ++i) dma16(rv, dst + 1024u * (kSknDma / 2 + i), voff[i]);
+    };
+
+    f16x8 qb[8];
+    const uint32_t grp = (uint32_t)lane >> 4, jl = (uint32_t)lane & 15u;
+    const uint32_t vrd = (4u * hh + (jl >> 2)) * kVP + 16u * (grp & 1u) + 4u * (jl & 3u);
+    // unit k is in buffer k % 2; while it is computed, unit k + 1's copy (16
+    // loads) may be in flight; once computed, its buffer takes unit k + 2.
+    // Unit 0 is peeled off the loop: the compiler's own waits for the Q loads
+    // (it does not see the copies, which its vmcnt values would then also
+    // drain) stay out of the loop.
+    auto step = [&](uint32_t k) {
+        if (k + 1 < nunits) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kSknDma));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        const uint32_t u = (uint32_t)wave + kSknWaves * k;
+        const f16* kt = reinterpret_cast<const f16*>(mine + (k & 1u) * kSknUnitBytes);
+        const f16* vt = kt + kSkUnit * kD;
+        // S^T = K . Q^T, online softmax, O^T += V^T . P^T
+        f32x16 s = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+            s = mfma32(lds16(kt + k_read_offset((uint32_t)n, (uint32_t)hh, (uint32_t)ks)), qb[ks], s);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float x = s[i];
+            if (u == last) {
+                // the diagonal unit starts at q0: mask keys past the query and past N
+                const uint32_t key = q0 + 8u * (uint32_t)(i >> 2) + 4u * hh + (uint32_t)(i & 3);
+                if (key > q0 + n || key >= N) x = -INFINITY;
+                s[i] = x;
+            }
+            mx = fmaxf(mx, x);
+        }
+        mx = fmaxf(mx, xor_lane(mx, 32));
+        const float m_tile = mx * a.scale_log2;
+        if (__any(m_tile > m_used + kRescaleSlack)) {
+            const float mn = (m_tile > m_used + kRescaleSlack) ? m_tile : m_used;
+            const float al = fast_exp2(m_used - mn);
+            l_run *= al;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[dt] *= al;
+            m_used = mn;
+        }
+        const float mneg = -m_used;
+        float psum = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            f16x8 va[4];
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const uint32_t vd = vrd + 32u * ((uint32_t)dt ^ (jl >> 2));
+                const f16x4 lo = lds_tr4(vt + vd + 16 * ks * kVP);
+                const f16x4 hi = lds_tr4(vt + vd + (16 * ks + 8) * kVP);
+                va[dt] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+            f16x8 pb;
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                pb[r] = (f16)fast_exp2(__builtin_fmaf(s[8 * ks + r], a.scale_log2, mneg));
+#pragma unroll
+            for (int r = 0; r < 8; r += 2) {
+                const f16x2 pair = {pb[r], pb[r + 1]};
+                psum = __builtin_amdgcn_fdot2(pair, f16x2{(f16)1.0f, (f16)1.0f}, psum, false);
+            }
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[dt] = mfma32(va[dt], pb, o[dt]);
+        }
+        l_run += psum;
+        // the unit's LDS reads have returned (their MFMAs consumed them), so
+        // its buffer can take unit k + 2
+        if (k + 2 < nunits) issue(u + 2u * kSknWaves, k & 1u);
+    };
+    // everything that uses Q in one block: the compiler's waits for the Q
+    // loads then stay in the peeled first unit on every path into the loop
+    if (nunits) {
+        // Q^T B operands (lane (hh, n): Q[q0 + n][head][16 s + 8 hh .. +7]),
+        // issued before the first copies; rows past N read as zero
+        const uint32_t q_row_bytes = (uint32_t)(a.q_stride * 2);
+        const BufRsrc rq = make_rsrc(a.q + (uint64_t)head * kD,
+                                     __builtin_amdgcn_readfirstlane((N - 1) * q_row_bytes + kD * 2));
+        const uint32_t qoff = (q0 + n) * q_row_bytes + 16u * hh;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) qb[s] = buf_ld16(rq, qoff + 32u * s);
+        issue((uint32_t)wave, 0u);
+        if (nunits > 1) issue((uint32_t)wave + kSknWaves, 1u);
+        step(0);
+        for (uint32_t k = 1; k < nunits; ++k) step(k);
+    }
+
+    const uint32_t query = q0 + n;
+    if (last == 0) {
+        const float inv = 1.f / (l_run + xor_lane(l_run, 32));
+        if (query < N) {
+            f16* orow = a.out + ((uint64_t)query * a.num_heads + head) * kD;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    f16x4 w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[e] = (f16)(o[dt][4 * i4 + e] * inv);
+                    *reinterpret_cast<f16x4*>(orow + 32 * dt + 8 * i4 + 4 * hh) = w;
+                }
+        }
+        return;
+    }
+    // The waves with units (0 .. min(3, last)) leave O^T in their buffer 0
+    // (16 KiB = 16 words x 64 lanes; every copy has landed and every read of
+    // it is done) and (m, l) in sml; m is finite (each wave's first unit
+    // holds a key <= every query of the tile).  Wave w then folds dims
+    // 32 w .. 32 w + 31 of every state.
+    const uint32_t nstates = last < (uint32_t)kSknWaves ? last + 1u : (uint32_t)kSknWaves;
+    if (nunits) {
+        f32x4* w = reinterpret_cast<f32x4*>(mine) + lane;
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            w[64 * e] = f32x4{o[e >> 2][4 * (e & 3)], o[e >> 2][4 * (e & 3) + 1],
+                              o[e >> 2][4 * (e & 3) + 2], o[e >> 2][4 * (e & 3) + 3]};
+        sml[wave][lane] = f32x2{m_used, l_run};
+    }
+    __syncthreads();
+    const int dt = wave;
+    float m = -INFINITY, l = 0.f;
+    f32x16 acc = f32x16{};
+    for (uint32_t w2 = 0; w2 < nstates; ++w2) {
+        const f32x4* w = reinterpret_cast<const f32x4*>(ub + w2 * 2 * kSknUnitBytes) + lane;
+        const f32x2 ml = sml[w2][lane];
+        f32x4 ow[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ow[q] = w[64 * (4 * dt + q)];
+        const float mx = fmaxf(m, ml[0]);  // ml[0] is finite
+        const float a1 = fast_exp2(m - mx), a2 = fast_exp2(ml[0] - mx);
+        l = l * a1 + ml[1] * a2;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = acc[i] * a1 + ow[i >> 2][i & 3] * a2;
+        m = mx;
+    }
+    const float inv = 1.f / (l + xor_lane(l, 32));
+    if (query < N) {
+        f16* orow = a.out + ((uint64_t)query * a.num_heads + head) * kD;
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+            f16x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = (f16)(acc[4 * i4 + e] * inv);
+            *reinterpret_cast<f16x4*>(orow + 32 * dt + 8 * i4 + 4 * hh) = w;
+        }
+    }
+}
+
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -745,6 +967,18 @@ hipError_t launch_prefill_kernel(const PrefillArgs& a0, int path, hipStream_t st
     const bool all = waves == 4 && a.seq_len <= kAllTiles * kBN &&
                      get_option(kOptPrefillStageAll) != 1;
     const long sk_opt = get_option(kOptPrefillSplitKeys);
+    const bool skn = sk_opt == 4 || (sk_opt == 0 && wopt == 0 && a0.seq_len > kAllTiles * kBN &&
+                                     a0.seq_len <= kSknMaxTokens);
+    if (skn) {
+        // one 4-wave workgroup per (head, 32-query tile), 32-key units streamed per wave
+        PrefillArgs b = a0;
+        b.q_tiles = (b.seq_len + kSkUnit - 1) / kSkUnit;
+        const uint64_t n_blocks = (uint64_t)b.q_tiles * b.num_heads;
+        if (n_blocks > 0x7fffffffull) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(prefill_skn, dim3((uint32_t)n_blocks), dim3(64 * kSknWaves), 0, stream,
+                           b);
+        return hipGetLastError();
+    }
     const bool sk = all && sk_opt != 1;
     // 32-key units over 8 waves only where one query tile needs no combine
     // (N <= 32: 4.1 against 4.6 us per graph launch); with several units

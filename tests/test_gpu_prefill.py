@@ -125,14 +125,16 @@ def test_prefill_8192_vs_oracle_rows_and_torch(attn, gpu):
 
 @pytest.mark.parametrize("N,prefixes,split_keys", [(700, (1, 64, 65, 333), 1),
                                                    (254, (1, 31, 64, 65, 200), 2),
-                                                   (254, (1, 31, 64, 65, 200), 3)])
+                                                   (254, (1, 31, 64, 65, 200), 3),
+                                                   (700, (1, 31, 33, 64, 65, 333), 4)])
 def test_prefill_prefix_invariance(attn, gpu, N, prefixes, split_keys):
     """Row t depends only on rows <= t: a prefill of N tokens and of a prefix
     of N' tokens agree bit for bit on the first N' rows -- across the
     pipelined and all-tiles-staged kernels (which compute the same tiles in
     the same order; the split-keys form is off), and within each split-keys
     form of short prompts (option value 2: 64-key tiles over 4 waves, 3:
-    32-key units over 8 waves; the same units combined the same way)."""
+    32-key units over 8 waves, 4: 32-key units streamed per wave; the same
+    units combined the same way)."""
     qkv, cache, stride = engine_inputs(N, seed=21)
     try:
         attn.set_option("prefill_split_keys", split_keys)
@@ -246,14 +248,15 @@ def test_prefill_four_and_eight_wave_tiles_identical(attn, gpu, N):
     assert_close(got, exp, 2e-3, 1e-2, f"N={N}")
 
 
-@pytest.mark.parametrize("form", [0, 2, 3])
+@pytest.mark.parametrize("form", [0, 2, 3, 4])
 @pytest.mark.parametrize("N", [1, 2, 31, 32, 33, 63, 64, 65, 96, 97, 128, 129, 191, 192, 200,
                                254, 255, 256])
 def test_prefill_split_keys_vs_oracle(attn, gpu, N, form):
     """Short prompts (N <= 256): one workgroup per head and 32-query tile,
     its keys split over the waves (form 2: 64-key tiles over 4 waves; form
-    3: 32-key units over 8 waves; form 0, the default: form 3 up to 32
-    tokens, form 2 above) and combined through LDS;
+    3: 32-key units over 8 waves; form 4: 32-key units streamed per wave;
+    form 0, the default: form 3 up to 32 tokens, form 2 above) and combined
+    through LDS;
     against the fp64 oracle, and against the sequential kernel (the same
     attention, combined in another order: within the tolerance)."""
     qkv, cache, stride = engine_inputs(N, seed=1300 + N)
@@ -282,7 +285,7 @@ def test_prefill_split_keys_other_heads(attn, gpu, Hq, Hkv, N):
     v = rng.standard_normal((N + 1) * kv_stride).astype(np.float16).view(np.uint16)
     _, e32 = oracle.attention(q, k, v, N, Hq, Hkv, D, q_stride, kv_stride, N, causal=True)
     try:
-        for form in (2, 3):
+        for form in (2, 3, 4):
             attn.set_option("prefill_split_keys", form)
             print(f"[case] prefill split keys Hq={Hq} Hkv={Hkv} N={N} form={form}", flush=True)
             out = torch.empty(N * Hq * D, dtype=torch.float16, device=gpu)
@@ -292,3 +295,29 @@ def test_prefill_split_keys_other_heads(attn, gpu, Hq, Hkv, N):
             assert_close(host(out), e32.reshape(-1), 2e-3, 1e-2, f"{Hq}/{Hkv} N={N} form={form}")
     finally:
         attn.set_option("prefill_split_keys", 0)
+
+
+@pytest.mark.parametrize("N", [257, 288, 300, 511, 512, 640, 777, 1024, 1500, 1536, 1537, 2049])
+def test_prefill_streaming_split_keys(attn, gpu, N):
+    """Prompts past the all-tiles forms: one workgroup per head and 32-query
+    tile whose 4 waves each stream every 4th 32-key unit (the default from
+    257 to 1536 tokens, option value 4 at any length); against the fp64
+    oracle (every row up to 1024 tokens, sampled rows above) and against the
+    4-head kernels (the same attention, combined in another order)."""
+    qkv, cache, stride = engine_inputs(N, seed=1700 + N)
+    rows = None if N <= 1024 else np.unique(np.concatenate([np.arange(0, N, 13), [N - 1]]))
+    exp = oracle_prefill(qkv, cache, N, stride, rows=rows).reshape(-1)
+    outs = {}
+    try:
+        for form in (0, 4, 1):
+            attn.set_option("prefill_split_keys", form)
+            print(f"[case] prefill streaming split keys N={N} form={form}", flush=True)
+            outs[form] = run_prefill(attn, gpu, qkv, cache, N, stride)
+    finally:
+        attn.set_option("prefill_split_keys", 0)
+    if N <= 1536:
+        assert np.array_equal(outs[0], outs[4])  # the default is the streaming form
+    for form in (0, 4):
+        got = outs[form] if rows is None else outs[form].reshape(N, -1)[rows].reshape(-1)
+        assert_close(got, exp, 2e-3, 1e-2, f"N={N} form={form}")
+    assert_close(outs[4], outs[1], 2e-3, 1e-2, f"N={N} vs the 4-head kernels")
