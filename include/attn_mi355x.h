@@ -348,7 +348,7 @@ int attn_prefill_plan(const void* q, const void* k, const void* v, const void* o
  * or 128 tokens per wave of the 256 x 128-tile MFMA GEMM), "qkv_gemm_wide"
  * (0 = automatic, from 7168 tokens; 1 = never; 2 = whenever N is a multiple
  * of 384 and Y is 16-byte aligned), "prefill_waves" (0 = automatic: 4-wave
- * workgroups of 32 queries up to 4096 tokens, 8-wave workgroups of 64 queries
+ * workgroups of 32 queries up to 6144 tokens, 8-wave workgroups of 64 queries
  * above; 4 or 8 forces one), "prefill_stage_all" (0 = automatic: up to 256
  * tokens every key tile of a 4-wave workgroup is copied into LDS at once;
  * 1 = never), "prefill_split_keys" (0 = automatic: up to 1536 tokens one

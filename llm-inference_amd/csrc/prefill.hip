@@ -941,11 +941,12 @@ int plan_prefill(const PrefillArgs& a) {
     return 1;
 }
 
-// 4-wave workgroups up to this many tokens (see prefill_d128): measured 10-23 %
-// faster than 8-wave ones from 64 to 2048 tokens, 2-10 % at 4096; from 4608
-// tokens the 8-wave tile wins (27 % at 8192), its two waves per SIMD hiding
-// each other's softmax once every CU has work
-constexpr uint32_t kFourWaveMaxTokens = 4096;
+// 4-wave workgroups up to this many tokens (see prefill_d128): with the MFMA
+// results in VGPRs, measured 8-20 % faster than 8-wave ones from 1664 to
+// 5120 tokens and 2-5 % at 6144 (162 against 170 us); from 7168 tokens the
+// 8-wave tile wins (205 against 222 us; 258 against 285 us at 8192), its two
+// waves per SIMD hiding each other's softmax once every CU has work
+constexpr uint32_t kFourWaveMaxTokens = 6144;
 
 hipError_t launch_prefill_kernel(const PrefillArgs& a0, int path, hipStream_t stream) {
     if (path != 1) return hipErrorInvalidValue;
