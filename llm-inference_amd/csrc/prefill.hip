@@ -312,11 +312,14 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
                 }
                 mx = fmaxf(mx, x);
             }
-        mx = fmaxf(mx, xor_lane(mx, 32));
-        const float m_tile = mx * a.scale_log2;
-        // one (rarely taken) block rescales, so none of it is speculated into
-        // the common path
-        if (__any(m_tile > m_used + kRescaleSlack)) {
+        // lanes n and n + 32 hold one query's keys and share m_used; the
+        // pair's maximum exceeds m_used + slack iff one lane's own maximum
+        // does, so the exchange of the two (an LDS round trip) is only made
+        // in the rescale block.  One (rarely taken) block rescales, so none of
+        // it is speculated into the common path.
+        const float m_lane = mx * a.scale_log2;
+        if (__any(m_lane > m_used + kRescaleSlack)) {
+            const float m_tile = fmaxf(m_lane, xor_lane(m_lane, 32));
             const float mn = (m_tile > m_used + kRescaleSlack) ? m_tile : m_used;
             const float al = fast_exp2(m_used - mn);
             l_run *= al;
@@ -808,9 +811,10 @@ __global__ __launch_bounds__(64 * kSknWaves, 1) void prefill_skn(PrefillArgs a) 
             }
             mx = fmaxf(mx, x);
         }
-        mx = fmaxf(mx, xor_lane(mx, 32));
-        const float m_tile = mx * a.scale_log2;
-        if (__any(m_tile > m_used + kRescaleSlack)) {
+        // the pair's exchange only in the rescale block, as in prefill_d128
+        const float m_lane = mx * a.scale_log2;
+        if (__any(m_lane > m_used + kRescaleSlack)) {
+            const float m_tile = fmaxf(m_lane, xor_lane(m_lane, 32));
             const float mn = (m_tile > m_used + kRescaleSlack) ? m_tile : m_used;
             const float al = fast_exp2(m_used - mn);
             l_run *= al;
