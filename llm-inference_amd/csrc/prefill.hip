@@ -20,7 +20,11 @@
 //    past N read as zero through the buffer range check.
 //  * S^T = K . Q^T with v_mfma_f32_32x32x16_f16: keys are MFMA rows, queries
 //    columns, so each lane holds one query's scores and the online softmax
-//    (running max, running sum, rescale) is per lane plus one xor-32 exchange.
+//    (running max, running sum, rescale) is per lane; the xor-32 exchange
+//    with the lane holding the query's other keys is made only when the
+//    running maximum moves.  Q is pre-scaled into the exp2 domain and the
+//    accumulators start at -m, so the MFMAs return the shifted scores and
+//    P = exp2(S) needs no multiply-add per score.
 //  * O^T = V^T . P^T on the same MFMA; O^T stays in 64 accumulator registers.
 //    The V^T operand comes from row-major V through ds_read_b64_tr_b16 (two
 //    4-key transposing reads per operand), with the keys in the order the
@@ -213,6 +217,25 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
     float m_used = -INFINITY, l_run = 0.f;
+    // kShift: scores leave the QK MFMAs in exp2 units and already shifted.
+    // Q is scaled by log2(e)/sqrt(D) once (rounded to fp16) and each tile's
+    // accumulators start at -m_cur (negm, 16 copies) instead of 0, so
+    // P = exp2(s) takes no per-score multiply-add (32 v_fma_f32 per wave and
+    // tile): C4 264.8 -> 256.9 us, 4096 tokens 94.5 -> 91.7 us.  m_cur is 0
+    // until the first rescale sets it to m_used; thr = m_used + slack - m_cur.
+    // The split-keys form (one tile per wave) keeps the multiply-add: there
+    // the one-time scaling of Q sits on the critical path (C2 +0.3 us).
+    constexpr bool kShift = !SK;
+    f32x16 negm = f32x16{};
+    float m_cur = 0.f, thr = -INFINITY;
+    auto scale_q = [&]() {
+        if constexpr (kShift) {
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qb[s][e] = (f16)((float)qb[s][e] * a.scale_log2);
+        }
+    };
 
     // LDS-DMA staging.  DMA instruction i of a tile fills LDS bytes
     // [1024 i, 1024 i + 1024) of the buffer; lane L writes 16-byte chunk
@@ -282,7 +305,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         // (iglp_opt 0): 8-wave tile at C4 261.7 against 265.8 us (median of
         // six 100-launch medians each, same box), identical bits
         if constexpr (WAVES == 8) __builtin_amdgcn_iglp_opt(0);
-        f32x16 s[2] = {f32x16{}, f32x16{}};
+        f32x16 s[2] = {negm, negm};
         // K operands are read one k-step ahead of their MFMAs (rows n and
         // n + 32 share the swizzle)
         f16x8 ka[2][2];
@@ -316,16 +339,35 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         // pair's maximum exceeds m_used + slack iff one lane's own maximum
         // does, so the exchange of the two (an LDS round trip) is only made
         // in the rescale block.  One (rarely taken) block rescales, so none of
-        // it is speculated into the common path.
-        const float m_lane = mx * a.scale_log2;
-        if (__any(m_lane > m_used + kRescaleSlack)) {
-            const float m_tile = fmaxf(m_lane, xor_lane(m_lane, 32));
-            const float mn = (m_tile > m_used + kRescaleSlack) ? m_tile : m_used;
-            const float al = fast_exp2(m_used - mn);
-            l_run *= al;
+        // it is speculated into the common path.  The scores are relative to
+        // m_cur: the block moves them, m_cur and negm to the new m_used.
+        if constexpr (kShift) {
+            if (__any(mx > thr)) {
+                const float m_tile = fmaxf(mx, xor_lane(mx, 32)) + m_cur;
+                const float mn = (m_tile > m_used + kRescaleSlack) ? m_tile : m_used;
+                const float al = fast_exp2(m_used - mn);
+                l_run *= al;
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) o[dt] *= al;
-            m_used = mn;
+                for (int dt = 0; dt < 4; ++dt) o[dt] *= al;
+                m_used = mn;
+                const float d = mn - m_cur;
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) s[mt] -= d;
+                m_cur = mn;
+                negm = -mn;
+                thr = kRescaleSlack;
+            }
+        } else {
+            const float m_lane = mx * a.scale_log2;
+            if (__any(m_lane > m_used + kRescaleSlack)) {
+                const float m_tile = fmaxf(m_lane, xor_lane(m_lane, 32));
+                const float mn = (m_tile > m_used + kRescaleSlack) ? m_tile : m_used;
+                const float al = fast_exp2(m_used - mn);
+                l_run *= al;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) o[dt] *= al;
+                m_used = mn;
+            }
         }
         const float mneg = -m_used;
         float psum = 0.f;
@@ -346,8 +388,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
             }
             f16x8 pb;
 #pragma unroll
-            for (int r = 0; r < 8; ++r)
-                pb[r] = (f16)fast_exp2(__builtin_fmaf(s[ks >> 1][8 * (ks & 1) + r], a.scale_log2, mneg));
+            for (int r = 0; r < 8; ++r) {
+                const float x = s[ks >> 1][8 * (ks & 1) + r];
+                if constexpr (kShift) pb[r] = (f16)fast_exp2(x);
+                else pb[r] = (f16)fast_exp2(__builtin_fmaf(x, a.scale_log2, mneg));
+            }
             // row sum of the fp16 weights the PV product uses, two per
             // v_dot2_f32_f16 (fp32 accumulate)
 #pragma unroll
@@ -394,6 +439,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
             // Q and K have landed once at most the kVDma V copies are
             // outstanding (loads complete in order); V is awaited before PV
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(kVDma));
+            scale_q();
             if (t < last)
                 tile_step(ktt, vtt, t, std::false_type{}, std::true_type{});
             else
@@ -460,6 +506,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         for (uint32_t t = 0; t <= last; ++t)
             stage(t * kBN, kt0 + t * (kBN * kKP), vt0 + t * (kBN * kVP));
         publish();
+        scale_q();
         {
 #pragma unroll 1
             for (uint32_t t = 0; t < last; ++t)
@@ -472,6 +519,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
     // last read before the previous barrier.
     stage(0, kt0, vt0);
     publish();
+    scale_q();
     uint32_t j = 0;
     for (; j + 2 <= last; j += 2) {
         stage((j + 1) * kBN, kt1, vt1);
