@@ -302,9 +302,12 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         constexpr bool kDiag = decltype(diag_tag)::value;
         constexpr bool kVWait = decltype(v_wait_tag)::value;
         // the compiler's interleaving strategy for LDS reads and MFMAs
-        // (iglp_opt 0): 8-wave tile at C4 261.7 against 265.8 us (median of
-        // six 100-launch medians each, same box), identical bits
-        if constexpr (WAVES == 8) __builtin_amdgcn_iglp_opt(0);
+        // (iglp_opt 0), identical bits: 8-wave tile at C4 261.7 against
+        // 265.8 us (median of six 100-launch medians each, same box); 4-wave
+        // tile at 2048 tokens 39.0 against 41.4 us, 3072 61.6 against 63.4
+        // us; the all-tiles-staged forms of short prompts are level or slower
+        // with it (254 tokens 8.2 against 8.1 us)
+        if constexpr (!ALL) __builtin_amdgcn_iglp_opt(0);
         f32x16 s[2] = {negm, negm};
         // K operands are read one k-step ahead of their MFMAs (rows n and
         // n + 32 share the swizzle)
