@@ -321,3 +321,57 @@ def test_prefill_streaming_split_keys(attn, gpu, N):
         got = outs[form] if rows is None else outs[form].reshape(N, -1)[rows].reshape(-1)
         assert_close(got, exp, 2e-3, 1e-2, f"N={N} form={form}")
     assert_close(outs[4], outs[1], 2e-3, 1e-2, f"N={N} vs the 4-head kernels")
+
+
+def growing_score_inputs(N, seed, Hq=16, Hkv=4, D=128, beta=20.0):
+    """Engine-layout inputs whose scores grow along the keys: every query row
+    is g + noise and key row j is (j / N) beta g + noise for a fixed g of
+    0.5s, so q.k rises by ~beta |g|^2 / N per key and a query's running
+    maximum keeps moving past the lazy-rescale slack."""
+    qkv, cache, stride = engine_inputs(N, seed)
+    rng = np.random.default_rng(seed + 1)
+    g = np.full(D, 0.5)
+    rows = qkv.view(np.float16).reshape(N, stride)
+    q = g + 0.3 * rng.standard_normal((N, Hq, D))
+    k = (np.arange(N)[:, None, None] / N) * beta * g + 0.3 * rng.standard_normal((N, Hkv, D))
+    rows[:, :Hq * D] = q.reshape(N, -1).astype(np.float16)
+    rows[:, Hq * D:Hq * D + Hkv * D] = k.reshape(N, -1).astype(np.float16)
+    kc = cache.view(np.float16)[:(N + 2) * Hkv * D].reshape(N + 2, Hkv * D)
+    kc[:N] = rows[:, Hq * D:Hq * D + Hkv * D]
+    return qkv, cache, stride
+
+
+@pytest.mark.parametrize("N,waves,split_keys", [(254, 0, 0), (254, 4, 1), (254, 8, 1),
+                                                (1000, 0, 0), (1000, 4, 1), (1000, 8, 1),
+                                                (4096, 0, 0)])
+def test_prefill_growing_scores_rescale(attn, gpu, N, waves, split_keys):
+    """The running maximum moves past the slack on many key tiles (checked
+    here on the inputs), so the rescale block -- which also shifts the tile's
+    scores and the accumulators' starting value in the long-prompt tiles --
+    runs again and again after the first tile; every form against the fp64
+    oracle (sampled rows at 4096 tokens)."""
+    qkv, cache, stride = growing_score_inputs(N, seed=900 + N)
+    # the last query's maximum per 64-key tile, in exp2 units: count the
+    # tiles whose maximum exceeds every earlier one by more than 8
+    x = qkv.view(np.float16).reshape(N, stride).astype(np.float64)
+    s = (x[N - 1, :128] @ x[:, 2048:2048 + 128].T) / np.sqrt(128) * np.log2(np.e)
+    tmax = [s[j:j + 64].max() for j in range(0, N, 64)]
+    m, moves = tmax[0], 0
+    for t in tmax[1:]:
+        if t > m + 8:
+            m, moves = t, moves + 1
+    assert moves >= (2 if N < 512 else 4), moves
+    rows = None if N <= 1024 else np.unique(np.concatenate([np.arange(0, N, 37), [N - 1]]))
+    exp = oracle_prefill(qkv, cache, N, stride, rows=rows).reshape(-1)
+    try:
+        attn.set_option("prefill_waves", waves)
+        attn.set_option("prefill_split_keys", split_keys)
+        print(f"[case] prefill growing scores N={N} waves={waves} split_keys={split_keys}",
+              flush=True)
+        got = run_prefill(attn, gpu, qkv, cache, N, stride)
+    finally:
+        attn.set_option("prefill_waves", 0)
+        attn.set_option("prefill_split_keys", 0)
+    if rows is not None:
+        got = got.reshape(N, -1)[rows].reshape(-1)
+    assert_close(got, exp, 2e-3, 1e-2, f"N={N} waves={waves} split_keys={split_keys}")
