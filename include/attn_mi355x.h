@@ -351,14 +351,18 @@ int attn_prefill_plan(const void* q, const void* k, const void* v, const void* o
  * workgroups of 32 queries up to 6144 tokens, 8-wave workgroups of 64 queries
  * above; 4 or 8 forces one), "prefill_stage_all" (0 = automatic: up to 256
  * tokens every key tile of a 4-wave workgroup is copied into LDS at once;
- * 1 = never), "prefill_split_keys" (0 = automatic: up to 1536 tokens one
+ * 1 = never), "prefill_split_keys" (0 = automatic: up to 1024 tokens one
  * workgroup per head and 32-query tile, its keys split over the waves and
  * combined through LDS, as 8 waves of 32 keys up to 32 tokens, 4 waves of
  * 64-key tiles up to 256 and 4 waves each streaming every 4th 32-key unit
- * above; 1 = never; 2 = 4 waves of 64-key tiles (up to 256 tokens); 3 = 8
- * waves of 32 keys (up to 256 tokens); 4 = the streaming form at any
- * length), "decode_out_proj_fused" (see attn_decode_out_proj).  Returns 0
- * or -1 for an unknown name. */
+ * above; 1 = never, also no key halves; 2 = 4 waves of 64-key tiles (up to
+ * 256 tokens); 3 = 8 waves of 32 keys (up to 256 tokens); 4 = the
+ * streaming form at any length), "prefill_key_halves" (0 = automatic: from
+ * 1025 to 4096 tokens, unless "prefill_waves" or "prefill_split_keys" is
+ * set, 8-wave workgroups of 32 queries x 4 heads whose two 4-wave groups
+ * take the even and the odd key tiles and combine through LDS; 1 = never;
+ * 2 = at any length), "decode_out_proj_fused" (see attn_decode_out_proj).
+ * Returns 0 or -1 for an unknown name. */
 int attn_set_option(const char* name, long value);
 
 /* Library build identification (static string). */

@@ -80,6 +80,7 @@ int attn_set_option(const char* name, long value) {
     else if (!std::strcmp(name, "decode_out_proj_fused")) which = kOptDecodeOutProjFused;
     else if (!std::strcmp(name, "prefill_stage_all")) which = kOptPrefillStageAll;
     else if (!std::strcmp(name, "prefill_split_keys")) which = kOptPrefillSplitKeys;
+    else if (!std::strcmp(name, "prefill_key_halves")) which = kOptPrefillKeyHalves;
     if (which < 0) return -1;
     g_options[which].store(value, std::memory_order_relaxed);
     return 0;

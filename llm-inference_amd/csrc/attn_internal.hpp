@@ -244,7 +244,8 @@ enum Option {
     kOptDecodeOutProjFused = 8,   // 1: attn_decode_out_proj runs the fused merge + o_proj kernel
     kOptPrefillStageAll = 9,      // 0 = automatic (N <= 256: all key tiles staged at once); 1 = never
     kOptPrefillSplitKeys = 10,    // 0 = automatic; 1 = never; 2 = 64-key tiles over 4 waves; 3 = 32-key units over 8 waves; 4 = 32-key units streamed per wave
-    kOptCount = 11
+    kOptPrefillKeyHalves = 11,    // 0 = automatic; 1 = never; 2 = 32-query tiles whose key tiles two 4-wave groups split
+    kOptCount = 12
 };
 long get_option(int which);
 

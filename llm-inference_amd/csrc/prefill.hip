@@ -36,11 +36,14 @@
 //    KV head's K/V stays in one L2.
 //  * Tile j+1 is copied into the other LDS buffer while tile j is computed;
 //    one barrier per tile.
-//  * Short prompts (N <= 1536) split each 32-query tile's keys over the waves
+//  * Short prompts (N <= 1024) split each 32-query tile's keys over the waves
 //    of one head's workgroup and combine the partial states through LDS
 //    (prefill_d128<4, true, true>: 64-key tiles over 4 waves, up to 256
 //    tokens; prefill_sk32: 32-key units over 8 waves, up to 32 tokens;
-//    prefill_skn: 32-key units streamed per wave, from 257 to 1536 tokens).
+//    prefill_skn: 32-key units streamed per wave, from 257 to 1024 tokens).
+//    From 1025 to 4096 tokens the 32-query tile of 4 heads is computed by 8
+//    waves whose two 4-wave groups split its key tiles (even and odd), with
+//    the two states combined through LDS (prefill_d128<8, false, false, true>).
 #include "attn_internal.hpp"
 
 #include <type_traits>
@@ -158,24 +161,33 @@ constexpr uint32_t kAllTiles = 4;
 // added), so the chain of up to 4 dependent tiles becomes one tile plus the
 // combine, and a short prompt gets 4x the workgroups (one per head instead
 // of per 4 heads): C2 (254 tokens) 10.1 -> 6.6 us, 64 tokens 6.3 -> 4.7 us.
-template <int WAVES, bool ALL, bool SK>
+// KS2 (WAVES = 8, streaming): a workgroup is a 32-query tile of 4 heads; wave
+// w computes head w % 4, and the group w / 4 takes the even or the odd key
+// tiles with its own softmax state, two tiles staged per step; the second
+// group's state is folded into the first's through LDS at the end.
+template <int WAVES, bool ALL, bool SK, bool KS2 = false>
 __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
     static_assert(!ALL || WAVES == 4, "the all-tiles variant is the 4-wave kernel");
     static_assert(!SK || ALL, "split keys needs every key tile staged at once");
+    static_assert(!KS2 || (WAVES == 8 && !ALL), "key halves: the 8-wave streaming tile");
     constexpr int kW = WAVES;
-    constexpr int kBMw = 8 * WAVES;                     // query tokens per workgroup
+    // query tokens per workgroup (KS2: 32 queries, the two 4-wave groups
+    // split the key tiles)
+    constexpr int kBMw = KS2 ? 32 : 8 * WAVES;
     constexpr int kDpw = (kMaxDma + WAVES - 1) / WAVES;   // DMA instructions per wave
     // two LDS buffers per operand as distinct objects, so the compiler can
     // tell a DMA into one buffer from the reads of the other (ALL: one buffer
-    // per key tile, all filled before any is read)
-    constexpr int kKBuf = ALL ? (int)kAllTiles * kBN * kKP : kBN * kKP;
-    constexpr int kVBuf = ALL ? (int)kAllTiles * kBN * kVP : kBN * kVP;
+    // per key tile, all filled before any is read; KS2: two key tiles per
+    // buffer, one per group)
+    constexpr int kTiles = ALL ? (int)kAllTiles : (KS2 ? 2 : 1);
+    constexpr int kKBuf = kTiles * kBN * kKP;
+    constexpr int kVBuf = kTiles * kBN * kVP;
     __shared__ __attribute__((aligned(16))) f16 kt0[kKBuf];
-    __shared__ __attribute__((aligned(16))) f16 kt1[ALL ? 8 : kBN * kKP];
+    __shared__ __attribute__((aligned(16))) f16 kt1[ALL ? 8 : kKBuf];
     __shared__ __attribute__((aligned(16))) f16 vt0[kVBuf];
-    __shared__ __attribute__((aligned(16))) f16 vt1[ALL ? 8 : kBN * kVP];
-    // split keys: each wave's (m, l) for the combine
-    __shared__ f32x2 sml[SK ? kAllTiles : 1][64];
+    __shared__ __attribute__((aligned(16))) f16 vt1[ALL ? 8 : kVBuf];
+    // split keys: each wave's (m, l) for the combine (KS2: the second group's)
+    __shared__ f32x2 sml[SK ? kAllTiles : (KS2 ? 4 : 1)][64];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -194,7 +206,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         if (!map_block(blockIdx.x, quads, a.q_tiles, quad, tile)) return;
         head = 4u * quad + (uint32_t)(wave & 3);
         g = (4u * quad) / a.group;
-        q0 = tile * kBMw + 32u * (uint32_t)(wave >> 2);
+        q0 = tile * kBMw + (KS2 ? 0u : 32u * (uint32_t)(wave >> 2));
     }
     // the query tile's last key tile, which holds its diagonal
     const uint32_t last = (tile * kBMw + kBMw - 1) / kBN;
@@ -504,6 +516,96 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
             }
             return;
         }
+    } else if constexpr (KS2) {
+        // Key tiles split over the two 4-wave groups: group gk = wave / 4
+        // computes tiles gk, gk + 2, gk + 4, ... of the workgroup's 32-query
+        // tile with its own softmax state.  Step s stages tiles 2s and 2s + 1
+        // side by side into buffer s & 1 (one barrier per step), so a query
+        // tile's chain of steps is half its chain of key tiles.
+        const uint32_t gk = (uint32_t)wave >> 2;
+        const uint32_t steps = (last + 2u) / 2u;
+        auto stage2 = [&](uint32_t st, f16* kt, f16* vt) {
+            stage(2u * st * kBN, kt, vt);
+            if (2u * st + 1u <= last) stage((2u * st + 1u) * kBN, kt + kBN * kKP, vt + kBN * kVP);
+        };
+        // steps before the last hold two full tiles
+        auto full = [&](uint32_t st, const f16* kt, const f16* vt) {
+            tile_step(kt + gk * (kBN * kKP), vt + gk * (kBN * kVP), 2u * st + gk,
+                      std::false_type{}, std::false_type{});
+        };
+        // the last step holds tile `last` (the diagonal) and, when `last` is
+        // odd, the full tile last - 1
+        auto final_step = [&](uint32_t st, const f16* kt, const f16* vt) {
+            const uint32_t j = 2u * st + gk;
+            if (j == last)
+                tile_step(kt + gk * (kBN * kKP), vt + gk * (kBN * kVP), j, std::true_type{},
+                          std::false_type{});
+            else if (j < last)
+                tile_step(kt + gk * (kBN * kKP), vt + gk * (kBN * kVP), j, std::false_type{},
+                          std::false_type{});
+        };
+        stage2(0, kt0, vt0);
+        publish();
+        scale_q();
+        uint32_t st = 0;
+        for (; st + 2 < steps; st += 2) {
+            stage2(st + 1, kt1, vt1);
+            full(st, kt0, vt0);
+            publish();
+            stage2(st + 2, kt0, vt0);
+            full(st + 1, kt1, vt1);
+            publish();
+        }
+        if (st + 1 < steps) {
+            stage2(st + 1, kt1, vt1);
+            full(st, kt0, vt0);
+            publish();
+            final_step(st + 1, kt1, vt1);
+        } else {
+            final_step(st, kt0, vt0);
+        }
+        // The second group hands (O^T, m, l) of its head to the first through
+        // LDS (16 KiB per head: heads 0-1 over the K buffer 0, 2-3 over the V
+        // buffer 0, once every wave is past its last tile's reads), and the
+        // first group folds it in: M = max(m_a, m_b), l and O^T scaled by
+        // 2^(m - M) and added.  A group without a tile (one-tile query tiles)
+        // holds m = -inf, l = 0, O = 0 and adds nothing.
+        const uint32_t hw = (uint32_t)wave & 3u;
+        __syncthreads();
+        if (gk == 1) {
+            auto put = [&](f16* base) {
+                f32x4* w = reinterpret_cast<f32x4*>(base) + (hw & 1u) * 1024u + (uint32_t)lane;
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    w[64 * e] = f32x4{o[e >> 2][4 * (e & 3)], o[e >> 2][4 * (e & 3) + 1],
+                                      o[e >> 2][4 * (e & 3) + 2], o[e >> 2][4 * (e & 3) + 3]};
+            };
+            if (hw < 2) put(kt0);
+            else put(vt0);
+            sml[hw][lane] = f32x2{m_used, l_run};
+        }
+        __syncthreads();
+        if (gk == 1) return;
+        {
+            const f32x2 ml = sml[hw][lane];
+            const float mm = fmaxf(m_used, ml[0]);  // m_used is finite: tile 0 is this group's
+            const float a1 = fast_exp2(m_used - mm), a2 = fast_exp2(ml[0] - mm);
+            l_run = l_run * a1 + ml[1] * a2;
+            auto fold = [&](const f16* base) {
+                const f32x4* w =
+                    reinterpret_cast<const f32x4*>(base) + (hw & 1u) * 1024u + (uint32_t)lane;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const f32x4 x = w[64 * e];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        o[e >> 2][4 * (e & 3) + i] = o[e >> 2][4 * (e & 3) + i] * a1 + x[i] * a2;
+                }
+            };
+            if (hw < 2) fold(kt0);
+            else fold(vt0);
+            m_used = mm;
+        }
     } else if constexpr (ALL) {
         // tiles 0..last (last < kAllTiles) side by side, one wait
         for (uint32_t t = 0; t <= last; ++t)
@@ -775,8 +877,9 @@ constexpr int kSknWaves = 4;
 // forms) it measured 25-35 % faster than the 4-head workgroups (288 tokens
 // 7.3 against 10.4 us, 1024 tokens 17.9 against 23.4 us), level at 1536
 // (32.0 against 32.4 us) and slower from 1664 (37.0 against 34.6 us), where
-// the 4x K/V reads of one-head workgroups outweigh their parallelism
-constexpr uint32_t kSknMaxTokens = 1536;
+// the 4x K/V reads of one-head workgroups outweigh their parallelism; from
+// 1025 tokens the key-halves tile is faster (1152 tokens 23.6 against 26.8 us)
+constexpr uint32_t kSknMaxTokens = 1024;
 constexpr int kSknUnitBytes = 2 * kSkUnit * kD * 2;       // K + V of 32 keys: 16 KiB
 constexpr int kSknDma = kSknUnitBytes / 1024;             // 16: 8 for K, then 8 for V
 
@@ -1003,6 +1106,20 @@ int plan_prefill(const PrefillArgs& a) {
 // waves per SIMD hiding each other's softmax once every CU has work
 constexpr uint32_t kFourWaveMaxTokens = 6144;
 
+// 32-query tiles whose key tiles two 4-wave groups split
+// (prefill_d128<8, false, false, true>), automatic in (kKhMinTokens,
+// kKhMaxTokens]: a 32-query workgroup's chain of steps is half its chain of
+// key tiles, so the long chains near the end of a mid-length prompt no
+// longer leave CUs idle once the short ones are done.  Measured against the
+// default forms on one box: 1152 tokens 23.6 against 26.8 us (prefill_skn),
+// 1536 27.6 against 33.3, 2048 35.0 against 39.4, 3072 53.0 against 63.9,
+// 4096 81.6 against 91.7 (4-wave tiles); 1024 tokens 21.8 against 20.0
+// (prefill_skn), 4608 110.5 against 108.3, 6144 177.4 against 166.7, 8192
+// 288 against 266 us (the 8-wave tile shares each K/V tile between twice the
+// queries).
+constexpr uint32_t kKhMinTokens = 1024;
+constexpr uint32_t kKhMaxTokens = 4096;
+
 hipError_t launch_prefill_kernel(const PrefillArgs& a0, int path, hipStream_t stream) {
     if (path != 1) return hipErrorInvalidValue;
     const long wopt = get_option(kOptPrefillWaves);
@@ -1023,6 +1140,26 @@ hipError_t launch_prefill_kernel(const PrefillArgs& a0, int path, hipStream_t st
     const bool all = waves == 4 && a.seq_len <= kAllTiles * kBN &&
                      get_option(kOptPrefillStageAll) != 1;
     const long sk_opt = get_option(kOptPrefillSplitKeys);
+    const long kh_opt = get_option(kOptPrefillKeyHalves);
+    const bool kh = kh_opt == 2 || (kh_opt == 0 && sk_opt == 0 && wopt == 0 &&
+                                    a0.seq_len > kKhMinTokens && a0.seq_len <= kKhMaxTokens);
+    if (kh) {
+        // 32-query tiles x 4 heads, 8 waves: the two 4-wave groups split the
+        // key tiles
+        PrefillArgs b = a0;
+        b.q_tiles = (b.seq_len + 31u) / 32u;
+        uint64_t kh_blocks;
+        if (quads <= 8 && (8 % quads) == 0) {
+            const uint32_t per = 8u / quads;
+            kh_blocks = 8ull * ((b.q_tiles + per - 1) / per);
+        } else {
+            kh_blocks = (uint64_t)b.q_tiles * quads;
+        }
+        if (kh_blocks > 0x7fffffffull) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((prefill_d128<8, false, false, true>), dim3((uint32_t)kh_blocks),
+                           dim3(512), 0, stream, b);
+        return hipGetLastError();
+    }
     const bool skn = sk_opt == 4 || (sk_opt == 0 && wopt == 0 && a0.seq_len > kAllTiles * kBN &&
                                      a0.seq_len <= kSknMaxTokens);
     if (skn) {

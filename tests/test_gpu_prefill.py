@@ -301,7 +301,7 @@ def test_prefill_split_keys_other_heads(attn, gpu, Hq, Hkv, N):
 def test_prefill_streaming_split_keys(attn, gpu, N):
     """Prompts past the all-tiles forms: one workgroup per head and 32-query
     tile whose 4 waves each stream every 4th 32-key unit (the default from
-    257 to 1536 tokens, option value 4 at any length); against the fp64
+    257 to 1024 tokens, option value 4 at any length); against the fp64
     oracle (every row up to 1024 tokens, sampled rows above) and against the
     4-head kernels (the same attention, combined in another order)."""
     qkv, cache, stride = engine_inputs(N, seed=1700 + N)
@@ -315,7 +315,7 @@ def test_prefill_streaming_split_keys(attn, gpu, N):
             outs[form] = run_prefill(attn, gpu, qkv, cache, N, stride)
     finally:
         attn.set_option("prefill_split_keys", 0)
-    if N <= 1536:
+    if N <= 1024:
         assert np.array_equal(outs[0], outs[4])  # the default is the streaming form
     for form in (0, 4):
         got = outs[form] if rows is None else outs[form].reshape(N, -1)[rows].reshape(-1)
@@ -375,3 +375,44 @@ def test_prefill_growing_scores_rescale(attn, gpu, N, waves, split_keys):
     if rows is not None:
         got = got.reshape(N, -1)[rows].reshape(-1)
     assert_close(got, exp, 2e-3, 1e-2, f"N={N} waves={waves} split_keys={split_keys}")
+
+
+@pytest.mark.parametrize("N", [1, 31, 32, 33, 64, 65, 96, 254, 257, 700, 1025, 2049, 3000])
+def test_prefill_key_halves(attn, gpu, N):
+    """32-query tiles whose key tiles the two 4-wave groups of an 8-wave
+    workgroup split (even and odd tiles, states combined through LDS; the
+    default from 1025 to 4096 tokens, option value 2 at any length): against
+    the fp64 oracle (sampled rows above 1024 tokens), against the 4-wave
+    tiles, and with a query's row independent of what follows it."""
+    qkv, cache, stride = engine_inputs(N, seed=2300 + N)
+    rows = None if N <= 1024 else np.unique(np.concatenate([np.arange(0, N, 11), [N - 1]]))
+    exp = oracle_prefill(qkv, cache, N, stride, rows=rows).reshape(-1)
+    try:
+        attn.set_option("prefill_key_halves", 2)
+        print(f"[case] prefill key halves N={N}", flush=True)
+        got = run_prefill(attn, gpu, qkv, cache, N, stride)
+        if N > 64:
+            # the first 64 tokens alone give the same rows
+            q2, c2, _ = engine_inputs(64, seed=2300 + N)
+            x = qkv.view(np.float16).reshape(N, stride)[:64].copy()
+            q2 = x.reshape(-1).view(np.uint16)
+            c2[:] = np.float16(123.0).view(np.uint16)
+            kv = c2.view(np.float16)
+            kv[:66 * 512].reshape(66, 512)[:64] = x[:, 2048:2560]
+            kv[66 * 512:].reshape(66, 512)[:64] = x[:, 2560:]
+            head = run_prefill(attn, gpu, q2, c2, 64, stride)
+            assert np.array_equal(head, got.reshape(N, -1)[:64].reshape(-1))
+        if 1024 < N <= 4096:
+            attn.set_option("prefill_key_halves", 0)
+            assert np.array_equal(run_prefill(attn, gpu, qkv, cache, N, stride), got)
+        attn.set_option("prefill_key_halves", 1)
+        attn.set_option("prefill_split_keys", 1)
+        attn.set_option("prefill_waves", 4)
+        ref = run_prefill(attn, gpu, qkv, cache, N, stride)
+    finally:
+        attn.set_option("prefill_key_halves", 0)
+        attn.set_option("prefill_split_keys", 0)
+        attn.set_option("prefill_waves", 0)
+    g = got if rows is None else got.reshape(N, -1)[rows].reshape(-1)
+    assert_close(g, exp, 2e-3, 1e-2, f"N={N}")
+    assert_close(got, ref, 2e-3, 1e-2, f"N={N} vs the 4-wave tiles")
