@@ -735,6 +735,13 @@ def main():
         p254 = bench_prefill_graph(torch, A, hipgraph, 254, steps, warmup)
         detail["prefill"]["254"] = {"us": p254 * 1e3, "TFLOPs": prefill_flops(254) / p254 / 1e9}
         log(f"prefill N=254: {p254 * 1e3:.1f} us")
+        # mid-length prompts (each length's automatic form), median of 60
+        # per-launch event timings after 20 warm-up launches
+        for Nx in (1024, 2048, 4096):
+            pm, (plo, _, phi) = bench_prefill(torch, A, Nx, 60, 20)
+            detail["prefill"][str(Nx)] = {"us": pm * 1e3, "TFLOPs": prefill_flops(Nx) / pm / 1e9,
+                                          "launches_us": [plo * 1e3, pm * 1e3, phi * 1e3]}
+            log(f"prefill N={Nx}: {pm * 1e3:.1f} us ({prefill_flops(Nx) / pm / 1e9:.0f} TFLOP/s)")
         f1 = bench_launch_floor(torch, A, hipgraph, 1, 128, steps, warmup)
         f2 = bench_launch_floor(torch, A, hipgraph, 2, 128, steps, warmup)
         detail["launch_floor"] = {"one_kernel_us": f1 * 1e3, "two_kernels_us": f2 * 1e3,
