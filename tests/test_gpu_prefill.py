@@ -416,3 +416,21 @@ def test_prefill_key_halves(attn, gpu, N):
     g = got if rows is None else got.reshape(N, -1)[rows].reshape(-1)
     assert_close(g, exp, 2e-3, 1e-2, f"N={N}")
     assert_close(got, ref, 2e-3, 1e-2, f"N={N} vs the 4-wave tiles")
+
+
+@pytest.mark.parametrize("Hq,Hkv,N", [(32, 4, 1500), (8, 2, 1100), (4, 1, 2049), (12, 3, 1300)])
+def test_prefill_key_halves_other_heads(attn, gpu, Hq, Hkv, N):
+    """The key-halves tile at other head counts (2, 8 and 3 head quads: the
+    XCD-pinned and the plain workgroup orders), forced and as the default,
+    against the fp64 oracle on sampled rows."""
+    qkv, cache, stride = engine_inputs(N, seed=2500 + N, Hq=Hq, Hkv=Hkv)
+    rows = np.unique(np.concatenate([np.arange(0, N, 17), [N - 1]]))
+    exp = oracle_prefill(qkv, cache, N, stride, Hq=Hq, Hkv=Hkv, rows=rows).reshape(-1)
+    try:
+        attn.set_option("prefill_key_halves", 2)
+        print(f"[case] prefill key halves Hq={Hq} Hkv={Hkv} N={N}", flush=True)
+        got = run_prefill(attn, gpu, qkv, cache, N, stride, Hq=Hq, Hkv=Hkv)
+    finally:
+        attn.set_option("prefill_key_halves", 0)
+    assert np.array_equal(run_prefill(attn, gpu, qkv, cache, N, stride, Hq=Hq, Hkv=Hkv), got)
+    assert_close(got.reshape(N, -1)[rows].reshape(-1), exp, 2e-3, 1e-2, f"{Hq}/{Hkv} N={N}")
