@@ -83,12 +83,9 @@ def rand16(torch, n, seed, sigma=1.0, device="cuda"):
 def time_graph(torch, A, hipgraph, launch_one, steps, warmup, stream, replays=7):
     """Warm up with `warmup` eager launches, capture `steps` launches into one
     graph, replay it once untimed, then `replays` times inside event brackets
-    on the launch stream.  Each timed replay is queued behind an untimed
-    replay of the same graph, so that its packets are all in the queue when
-    its first event executes: hipGraphLaunch takes ~10 us on the host before
-    the first kernel is enqueued, which an idle GPU would otherwise count
-    (~0.5 us per call in a 20-call graph).  Returns ms per launch of the
-    median replay and the (min, median, max) over the replays."""
+    on the launch stream, each bracketed by synchronizations.  Returns ms per
+    launch of the median replay and the (min, median, max) over the
+    replays."""
     sp = stream.cuda_stream
     with torch.cuda.stream(stream):
         for i in range(warmup):
@@ -106,7 +103,6 @@ def time_graph(torch, A, hipgraph, launch_one, steps, warmup, stream, replays=7)
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
-            hipgraph.launch(exe, sp)  # untimed: keeps the GPU busy while the rest is queued
             e0.record(stream)
             hipgraph.launch(exe, sp)
             e1.record(stream)
