@@ -81,17 +81,26 @@ __device__ __forceinline__ f32x4 buf_ldf4(BufRsrc r, uint32_t byte_off) {
 // from moving stores across
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// The split kernel: grid (nsplit, Hkv / HPW); workgroup (c, grp) owns chunk c
-// of KV heads HPW*grp .. HPW*grp + HPW-1.  Wave w serves KV head
-// HPW*grp + w % HPW and every (8/HPW)-th batch of the chunk, so the waves of a
-// workgroup read whole cache-row segments together.
+// The split kernel: workgroup (grp, c) owns chunk c of KV heads HPW*grp ..
+// HPW*grp + HPW-1.  Wave w serves KV head HPW*grp + w % HPW and every
+// (8/HPW)-th batch of the chunk, so the waves of a workgroup read whole
+// cache-row segments together.  Grid order (decode_grid): while a chunk is at
+// most two batches per wave (every load of the call is issued at once) the
+// grid is (Hkv / HPW, nsplit), so the head groups of one chunk are
+// consecutive workgroups and the round-robin dispatch over the 8 XCDs gives
+// each XCD chunks of one head group: 15.65-15.68 against 16.02-16.08 us per
+// call at L = 32768 with the chunks consecutive (grid (nsplit, Hkv / HPW),
+// each XCD then taking both halves of the same cache rows), level at 254,
+// 4096 and 16384 keys.  Longer chunks keep (nsplit, Hkv / HPW): level from
+// 40960 to 98304 keys, but 26.3-27.9 against 25.9-26.3 us at 65536.
 template <int HPW, bool ROPE>
 __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
-    const uint32_t c = blockIdx.x;
-    const uint32_t grp = blockIdx.y;
     constexpr int WAVES = 8;
     constexpr int kThreads = WAVES * 64;
     constexpr int kPhases = WAVES / HPW;  // waves sharing one KV head
+    const bool head_groups_inner = a.chunk <= 64u * kPhases;
+    const uint32_t grp = head_groups_inner ? blockIdx.x : blockIdx.y;
+    const uint32_t c = head_groups_inner ? blockIdx.y : blockIdx.x;
     __shared__ float s_m[WAVES][16];
     __shared__ float s_l[WAVES][16];
     __shared__ float s_acc[WAVES][16][kAccPitch];
@@ -485,7 +494,12 @@ DecodePlan replan_decode(DecodeArgs& a, int device) {
     return p;
 }
 
-dim3 decode_grid(const DecodeArgs& a, const DecodePlan& p) { return dim3(a.nsplit, p.groups); }
+// the split kernel's grid: head groups inner while a chunk is at most two
+// batches per wave (flash_decode_split derives the same order from a.chunk)
+dim3 decode_grid(const DecodeArgs& a, const DecodePlan& p) {
+    const uint32_t phases = 8u / (uint32_t)decode_hpw(p.path);
+    return a.chunk <= 64u * phases ? dim3(p.groups, a.nsplit) : dim3(a.nsplit, p.groups);
+}
 
 hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,
                                bool rope) {
