@@ -28,6 +28,7 @@ in detail.  Inputs are seeded synthetic N(0, sigma) tensors.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
        python bench.py --profile   (eager launches for rocprofv3 counter passes)
+       python bench.py --timeline  (per-segment decode timeline, instrumented library)
 """
 from __future__ import annotations
 
@@ -654,6 +655,108 @@ def profile_workload(torch, A):
     log("profile: 3 device copies of 256 MiB (reads 268435456 B, writes 268435456 B each)")
 
 
+def decode_timeline(torch, A, hipgraph, steps=20, warmup=5):
+    """Per-segment timeline of decode calls from the instrumented library
+    (libattn_timeline.so: the product's sources compiled with
+    ATTN_DECODE_TIMELINE, whose split and merge kernels store s_memrealtime
+    stamps, 100 MHz, at fixed points of every workgroup).  Each length runs
+    as bench_decode runs it (graph of `steps` calls, cold over 8 rotated KV
+    buffers from 4096 keys); the records of the last replay's calls 2..steps
+    are reduced per call relative to the call's first split workgroup entry,
+    then the median over the calls is reported.  Also: the plain streaming
+    read of the same bytes, cold and warm (one buffer, MALL-resident)."""
+    import ctypes
+    import numpy as np
+    lib = A.lib()
+    lib.attn_timeline_set.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    lib.attn_timeline_set.restype = ctypes.c_int
+    lib.attn_timeline_slot_words.argtypes = []
+    lib.attn_timeline_slot_words.restype = ctypes.c_size_t
+    words = lib.attn_timeline_slot_words()
+    split_words, merge_base = 16, 16 * 1024
+    slots = warmup + steps + 1
+    buf = torch.zeros(slots * words, dtype=torch.int64, device="cuda")
+    tick_us = 0.01  # s_memrealtime: 100 MHz
+    out = {"what": "instrumented build (libattn_timeline.so); us after the first split "
+                   "workgroup's entry, median over the calls of the last replay",
+           "lengths": {}}
+    for L in (32768, 65536, 16384, 4096, 254):
+        plan = A.decode_plan(L, HQ, HKV, D, KV_DIM)
+        groups = HKV // {1: 4, 2: 2, 3: 1}[plan["path"]]
+        nsplit_wg = groups * plan["nsplit"]
+        nmerge = HQ * (D // 4)
+        buf.zero_()
+        torch.cuda.synchronize()
+        assert lib.attn_timeline_set(buf.data_ptr(), slots) == 0
+        ms, _ = bench_decode(torch, A, hipgraph, L, 8 if L >= 4096 else 1, steps, warmup)
+        rec = buf.view(slots, words).cpu().numpy()
+        calls = []
+        for s in range(warmup + 1, warmup + steps):
+            r = rec[s]
+            sp = r[:split_words * nsplit_wg].reshape(nsplit_wg, split_words).astype(np.float64)
+            mg = r[merge_base:merge_base + 4 * nmerge].reshape(nmerge, 4).astype(np.float64)
+            t0 = sp[:, 0].min()
+            rel = lambda x: (x - t0) * tick_us  # noqa: E731
+            wc = sp[:, 2:10]
+            wc_any = wc[wc > 0]
+            wg_comp = wc.max(axis=1)           # each workgroup's last wave computed
+            last_wg = int(np.argmax(sp[:, 11]))  # the workgroup whose stores were acked last
+            c = {
+                "split_entry_last": rel(sp[:, 0].max()),
+                "loads_issued_median": rel(np.median(sp[:, 1])),
+                "loads_issued_last": rel(sp[:, 1].max()),
+                "wave_computed_first": rel(wc_any.min()),
+                "wave_computed_median": rel(np.median(wc_any)),
+                "wave_computed_last": rel(wc_any.max()),
+                "barrier_passed_last": rel(sp[:, 14].max()),
+                "fold_done_last": rel(sp[:, 10].max()),
+                "stores_acked_last": rel(sp[:, 11].max()),
+                "wg_barrier_after_last_wave_median": float(np.median(sp[:, 14] - wg_comp)) * tick_us,
+                "wg_fold_after_barrier_median": float(np.median(sp[:, 10] - sp[:, 14])) * tick_us,
+                "wg_acked_after_fold_median": float(np.median(sp[:, 11] - sp[:, 10])) * tick_us,
+                "last_wg_computed": rel(wg_comp[last_wg]),
+                "last_wg_barrier": rel(sp[last_wg, 14]),
+                "last_wg_fold": rel(sp[last_wg, 10]),
+                "merge_entry_first": rel(mg[:, 0].min()),
+                "merge_entry_last": rel(mg[:, 0].max()),
+                "merge_states_folded_median": rel(np.median(mg[:, 1])),
+                "merge_states_folded_last": rel(mg[:, 1].max()),
+                "merge_stored_last": rel(mg[:, 2].max()),
+            }
+            if s + 1 < warmup + steps:
+                nxt = rec[s + 1][:split_words * nsplit_wg].reshape(nsplit_wg, split_words)
+                c["next_call_split_entry"] = rel(float(nxt[:, 0].min()))
+            xcc = sp[:, 13].astype(int)
+            c["wave_computed_last_per_xcd"] = {int(x): rel(wg_comp[xcc == x].max())
+                                               for x in np.unique(xcc)}
+            calls.append(c)
+        med = {}
+        for k in calls[0]:
+            if k == "wave_computed_last_per_xcd":
+                med[k] = {x: float(np.median([cc[k][x] for cc in calls]))
+                          for x in calls[0][k]}
+            else:
+                vals = [cc[k] for cc in calls if k in cc]
+                med[k] = float(np.median(vals))
+        xcc0 = rec[warmup + 1][:split_words * nsplit_wg].reshape(nsplit_wg, split_words)[:, 13]
+        med["split_workgroups_per_xcd"] = {int(x): int((xcc0 == x).sum()) for x in np.unique(xcc0)}
+        med["us_per_call_instrumented"] = ms * 1e3
+        med["plan"] = plan
+        out["lengths"][str(L)] = med
+        log(f"timeline L={L}: {ms * 1e3:.2f} us per call (instrumented); "
+            + ", ".join(f"{k} {v:.2f}" for k, v in med.items() if isinstance(v, float)))
+    for L in (32768, 65536, 4096):
+        cold, _ = bench_read_ceiling(torch, A, hipgraph, L, 8, steps, warmup)
+        warm, _ = bench_read_ceiling(torch, A, hipgraph, L, 1, steps, warmup)
+        out.setdefault("read_ceiling", {})[str(L)] = {"cold_us": cold * 1e3, "warm_us": warm * 1e3}
+        log(f"read ceiling L={L}: cold {cold * 1e3:.2f} us, warm {warm * 1e3:.2f} us")
+    for wgs in (256, 512, 2048):
+        cold, _ = bench_read_ceiling(torch, A, hipgraph, 32768, 8, steps, warmup, wgs=wgs)
+        out["read_ceiling"]["32768"][f"cold_us_{wgs}_workgroups"] = cold * 1e3
+        log(f"read ceiling L=32768, {wgs} workgroups: cold {cold * 1e3:.2f} us")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -667,6 +770,9 @@ def main():
                          "QKV projections (GEMV, fused), 3 + 3 prefill QKV projections at 8192 "
                          "tokens (GEMM, fused) and a 256 MiB device copy that calibrates the "
                          "byte counters")
+    ap.add_argument("--timeline", action="store_true",
+                    help="per-segment timeline of decode calls from the instrumented library "
+                         "(libattn_timeline.so), plus the streaming read cold and warm")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the attention hot path is "
@@ -677,12 +783,17 @@ def main():
     import torch
     import attn_mi355x as A
     from attn_mi355x import hipgraph
+    if args.timeline:
+        A.LIB_PATH = A.PKG_ROOT / "lib" / "libattn_timeline.so"
     A.lib()
     props = torch.cuda.get_device_properties(0)
     log(f"device {props.name} {props.gcnArchName} CUs={props.multi_processor_count}")
     steps, warmup = args.steps, args.warmup
     if args.profile:
         profile_workload(torch, A)
+        return
+    if args.timeline:
+        print(json.dumps({"timeline": decode_timeline(torch, A, hipgraph)}), flush=True)
         return
 
     # ---- headline: C3 decode at L=32768, cold (8 rotated KV buffers)

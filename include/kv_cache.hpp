@@ -5,6 +5,32 @@
 //   t*Hkv*D + h*D (the kv_stride the attention launchers receive).
 // The constructor takes any config object exposing num_layers, max_seq_len,
 // num_kv_heads and head_dim (the reference passes its ModelConfig).
+//
+// The KVCache interface, layout arithmetic and capacity error text follow
+// include/kv_cache.hpp:8-82 of
+// MarcVivas/llm-inference, which is distributed under this notice:
+//
+//   MIT License
+//
+//   Copyright (c) 2026 MarcVivas
+//
+//   Permission is hereby granted, free of charge, to any person obtaining a copy
+//   of this software and associated documentation files (the "Software"), to deal
+//   in the Software without restriction, including without limitation the rights
+//   to use, copy, modify, merge, publish, distribute, sublicense, and/or sell
+//   copies of the Software, and to permit persons to whom the Software is
+//   furnished to do so, subject to the following conditions:
+//
+//   The above copyright notice and this permission notice shall be included in all
+//   copies or substantial portions of the Software.
+//
+//   THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND, EXPRESS OR
+//   IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF MERCHANTABILITY,
+//   FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT. IN NO EVENT SHALL THE
+//   AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM, DAMAGES OR OTHER
+//   LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR OTHERWISE, ARISING FROM,
+//   OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE USE OR OTHER DEALINGS IN THE
+//   SOFTWARE.
 #pragma once
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>

@@ -3,6 +3,32 @@
 // [max_seq_len][head_dim/2], inv_freq[i] = 1/powf(theta, 2i/D),
 // angle = float(pos) * inv_freq[i], cos/sin in fp32 rounded to fp16.  The
 // host tables are produced by attn_rope_tables() of libattn_mi355x.so.
+//
+// The RopeCache holder and compute_inverse_frequencies follow
+// include/rope_cache.hpp:9-60 of
+// MarcVivas/llm-inference, which is distributed under this notice:
+//
+//   MIT License
+//
+//   Copyright (c) 2026 MarcVivas
+//
+//   Permission is hereby granted, free of charge, to any person obtaining a copy
+//   of this software and associated documentation files (the "Software"), to deal
+//   in the Software without restriction, including without limitation the rights
+//   to use, copy, modify, merge, publish, distribute, sublicense, and/or sell
+//   copies of the Software, and to permit persons to whom the Software is
+//   furnished to do so, subject to the following conditions:
+//
+//   The above copyright notice and this permission notice shall be included in all
+//   copies or substantial portions of the Software.
+//
+//   THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND, EXPRESS OR
+//   IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF MERCHANTABILITY,
+//   FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT. IN NO EVENT SHALL THE
+//   AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM, DAMAGES OR OTHER
+//   LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR OTHERWISE, ARISING FROM,
+//   OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE USE OR OTHER DEALINGS IN THE
+//   SOFTWARE.
 #pragma once
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>

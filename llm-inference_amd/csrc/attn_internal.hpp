@@ -117,7 +117,29 @@ struct DecodeArgs {
     const f16* sin_t;
     uint32_t row;        // cache row of the new token (start_pos, patched)
     uint32_t apply;      // 1: rotate q and K; 0: copy K and V only (patched)
+#if defined(ATTN_DECODE_TIMELINE)
+    // instrumented build (libattn_timeline.so) only: this call's record of
+    // per-workgroup timestamps, set by the launchers
+    uint64_t* tl;
+#endif
 };
+
+#if defined(ATTN_DECODE_TIMELINE)
+// Record layout of one decode call (64-bit words): split workgroup w at
+// 16 w: [0] entry, [1] first K/V loads issued (wave 0), [2 + wave] that
+// wave's last batch computed (0: the wave had no keys), [14] every wave's
+// state in LDS (after the barrier), [10] thread 0's share of the fold done
+// and its partial stores issued, [11] those stores acknowledged, [12] HW_ID,
+// [13] XCC_ID; merge workgroup m at kTlMergeBase + 4 m: [0] entry, [1]
+// partial states loaded and folded, [2] output stored and acknowledged,
+// [3] XCC_ID.  Times are s_memrealtime ticks (100 MHz).  No wait or barrier
+// is added to the kernels except thread 0's wait for its own stores.
+constexpr uint32_t kTlSplitWords = 16;
+constexpr uint32_t kTlMaxSplitWgs = 1024;
+constexpr uint32_t kTlMergeBase = kTlSplitWords * kTlMaxSplitWgs;
+constexpr uint32_t kTlMaxMergeWgs = 1024;
+constexpr uint32_t kTlSlotWords = kTlMergeBase + 4 * kTlMaxMergeWgs;
+#endif
 
 // q head h (D = 128) rotated in place by lanes 0..7 of the calling threads
 // (lane e: pairs 8e..8e+7 and their partners 64 + 8e..), as

@@ -81,6 +81,18 @@ __device__ __forceinline__ f32x4 buf_ldf4(BufRsrc r, uint32_t byte_off) {
 // from moving stores across
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Timestamps of the instrumented build (libattn_timeline.so, compiled with
+// ATTN_DECODE_TIMELINE): TL(...) vanishes from the product library.
+#if defined(ATTN_DECODE_TIMELINE)
+#define TL(...) __VA_ARGS__
+__device__ __forceinline__ uint64_t tl_now() { return __builtin_amdgcn_s_memrealtime(); }
+// s_getreg_b32 of HW_ID (hwreg 4, 32 bits) and XCC_ID (hwreg 20, 4 bits)
+__device__ __forceinline__ uint64_t tl_hw_id() { return (uint32_t)__builtin_amdgcn_s_getreg(4 | (31 << 11)); }
+__device__ __forceinline__ uint64_t tl_xcc_id() { return (uint32_t)__builtin_amdgcn_s_getreg(20 | (3 << 11)); }
+#else
+#define TL(...)
+#endif
+
 // The split kernel: workgroup (grp, c) owns chunk c of KV heads HPW*grp ..
 // HPW*grp + HPW-1.  Wave w serves KV head HPW*grp + w % HPW and every
 // (8/HPW)-th batch of the chunk, so the waves of a workgroup read whole
@@ -103,7 +115,7 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     const uint32_t c = head_groups_inner ? blockIdx.y : blockIdx.x;
     __shared__ float s_m[WAVES][16];
     __shared__ float s_l[WAVES][16];
-    __shared__ float s_acc[WAVES][16][kAccPitch];
+    __shared__ __attribute__((aligned(16))) float s_acc[WAVES][16][kAccPitch];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -115,6 +127,14 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     // a grid wider than the KV heads (a graph node re-planned for another
     // heads-per-workgroup count) has nothing for its extra workgroups
     if (grp * HPW >= a.num_kv_heads) return;
+    TL(const uint64_t tl_t0 = tl_now();
+       uint64_t* const tl = a.tl + (uint64_t)(blockIdx.y * gridDim.x + blockIdx.x) * kTlSplitWords;
+       if (tid == 0) {
+           tl[0] = tl_t0;
+           tl[12] = tl_hw_id();
+           tl[13] = tl_xcc_id();
+       }
+       if (lane == 0) tl[2 + wave] = 0;)
     const uint32_t g = grp * HPW + hw;
     const uint32_t G = a.group;
     const uint32_t t0 = c * a.chunk;
@@ -220,6 +240,7 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
         KVBatch A, B;
         load(b, A);
         load(b + kStep, B);
+        TL(if (tid == 0) tl[1] = tl_now();)
 
         if constexpr (ROPE) {
             // dims 32s + 8gq + i (s = 0, 1) pair with 64 more (s + 2): the lane
@@ -297,45 +318,65 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
         compute(A, b);
         __builtin_amdgcn_sched_barrier(0);
         if (b + kStep < nk) compute(B, b + kStep);  // keys past the chunk are masked (p = 0)
+        TL(if (lane == 0) tl[2 + wave] = tl_now();)
     }
 
     // per-query sum over the four lane groups (the max is already shared)
     l_run += xor_lane(l_run, 16);
     l_run += xor_lane(l_run, 32);
-    if (gq == 0) {
-        s_m[wave][n] = m_run;
-        s_l[wave][n] = l_run;
+    // only the G columns that are query heads go to LDS: lane (gq, n < G)
+    // holds dims 32gq .. 32gq + 31 of query n (tile mt, row 4gq + i = dim
+    // 8(4gq + i) + mt), written as 16-byte rows
+    if ((uint32_t)n < G) {
+        if (gq == 0) {
+            s_m[wave][n] = m_run;
+            s_l[wave][n] = l_run;
+        }
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s_acc[wave][n][32 * gq + 8 * i + mt] = acc[mt][i];
     }
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s_acc[wave][n][32 * gq + 8 * i + mt] = acc[mt][i];
     __syncthreads();
+    TL(if (tid == 0) tl[14] = tl_now();)
 
-    // fold the kPhases waves of each KV head and write its partials
-    for (uint32_t idx = tid; idx < HPW * G * kD; idx += kThreads) {
-        const uint32_t hl = idx / (G * kD);
-        const uint32_t rem = idx - hl * G * kD;
-        const uint32_t qn = rem >> 7;
-        const uint32_t d = rem & (kD - 1);
+    // fold the kPhases waves of each KV head and write its partials: thread
+    // idx handles 4 consecutive dims of one (head, query) state, stored with
+    // one 16-byte buffer store (the range covers this workgroup's head group)
+    const uint32_t rows = HPW * G;  // states of this workgroup, (head, query) order
+    const BufRsrc rpo = make_rsrc(a.part_out + (uint64_t)grp * rows * a.nstate * kD,
+                                  rows * a.nstate * kD * 4u);
+    for (uint32_t idx = tid; idx < rows * (kD / 4); idx += kThreads) {
+        const uint32_t row = idx >> 5;  // kD / 4 = 32 items per state
+        const uint32_t hl = row / G;
+        const uint32_t qn = row - hl * G;
+        const uint32_t d = (idx & 31u) * 4u;
         float M = s_m[hl][qn];
 #pragma unroll
         for (int ph = 1; ph < kPhases; ++ph) M = fmaxf(M, s_m[hl + HPW * ph][qn]);
-        float num = 0.f, den = 0.f;
+        f32x4 num = {0.f, 0.f, 0.f, 0.f};
+        float den = 0.f;
 #pragma unroll
         for (int ph = 0; ph < kPhases; ++ph) {
             const int w = hl + HPW * ph;
             const float wt = fast_exp2(s_m[w][qn] - M);  // waves without keys: 0
-            num += wt * s_acc[w][qn][d];
+            num += wt * *reinterpret_cast<const f32x4*>(&s_acc[w][qn][d]);
             den += wt * s_l[w][qn];
         }
-        const uint64_t st = (uint64_t)((grp * HPW + hl) * G + qn) * a.nstate + c;
-        a.part_out[st * kD + d] = num;
+        const uint32_t st = row * a.nstate + c;  // state index within the head group
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, num), rpo,
+                                               (int)((st * kD + d) * 4u), 0, 0);
         if (d == 0) {
-            a.part_max[st] = M;
-            a.part_sum[st] = den;
+            const uint64_t sg = (uint64_t)grp * rows * a.nstate + st;
+            a.part_max[sg] = M;
+            a.part_sum[sg] = den;
         }
     }
+    TL(if (tid == 0) {
+           tl[10] = tl_now();
+           wait_stores();
+           tl[11] = tl_now();
+       })
 }
 
 constexpr int kMergeDims = 4;    // output dims per merge workgroup (one wave)
@@ -353,6 +394,11 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
     const uint32_t h = blockIdx.x;
     const uint32_t d0 = blockIdx.y * kMergeDims;
     const uint32_t S = a.nstate;
+    TL(uint64_t* const tl = a.tl + kTlMergeBase + 4u * (uint64_t)(blockIdx.y * gridDim.x + blockIdx.x);
+       if (lane == 0) {
+           tl[0] = tl_now();
+           tl[3] = tl_xcc_id();
+       })
     const BufRsrc rpm = make_rsrc(a.part_max + (uint64_t)h * S, S * 4u);
     const BufRsrc rps = make_rsrc(a.part_sum + (uint64_t)h * S, S * 4u);
     const BufRsrc rpo = make_rsrc(a.part_out + (uint64_t)h * S * kD, S * kD * 4u);
@@ -387,6 +433,7 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
         }
         m = mn;
     }
+    TL(if (lane == 0) tl[1] = tl_now();)
     // lanes without splits hold m = -inf and get weight 0
     const float mx = wave_max(m);
     const float w = fast_exp2(m - mx);
@@ -401,6 +448,7 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
         for (int e = 1; e < 4; ++e) v = lane == (uint32_t)e ? num[e] : v;
         a.out[(uint64_t)h * kD + d0 + lane] = (f16)(v / den);
     }
+    TL(wait_stores(); if (lane == 0) tl[2] = tl_now();)
     if constexpr (ROPE) {
         // every split workgroup has read q (the kernel boundary orders this)
         if (a.apply && blockIdx.y < 8 && lane == 0) rotate_q_head(a, h, blockIdx.y);
@@ -501,18 +549,64 @@ dim3 decode_grid(const DecodeArgs& a, const DecodePlan& p) {
     return a.chunk <= 64u * phases ? dim3(p.groups, a.nsplit) : dim3(a.nsplit, p.groups);
 }
 
+#if defined(ATTN_DECODE_TIMELINE)
+// instrumented build: each split launch takes the next of `tl_slots` records
+// (round robin), its merge launch the same one
+namespace {
+uint64_t* tl_base = nullptr;
+uint32_t tl_slots = 0, tl_next = 0, tl_cur = 0;
+uint64_t* tl_record(bool next) {
+    if (!tl_base || tl_slots == 0) return nullptr;
+    if (next) {
+        tl_cur = tl_next;
+        tl_next = (tl_next + 1) % tl_slots;
+    }
+    return tl_base + (uint64_t)tl_cur * kTlSlotWords;
+}
+}  // namespace
+#endif
+
 hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,
                                bool rope) {
     if (p.path < 1 || p.path > 3) return hipErrorInvalidValue;
     const void* fn = decode_split_symbol(p.path, rope);
+#if defined(ATTN_DECODE_TIMELINE)
+    DecodeArgs t = a;
+    t.tl = tl_record(true);
+    const dim3 grid = decode_grid(a, p);
+    if (!t.tl || grid.x * grid.y > kTlMaxSplitWgs) return hipErrorInvalidValue;
+    void* args[1] = {&t};
+    return hipLaunchKernel(fn, grid, dim3(512), args, 0, stream);
+#else
     void* args[1] = {const_cast<DecodeArgs*>(&a)};
     return hipLaunchKernel(fn, decode_grid(a, p), dim3(512), args, 0, stream);
+#endif
 }
 
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream, bool rope) {
+#if defined(ATTN_DECODE_TIMELINE)
+    DecodeArgs t = a;
+    t.tl = tl_record(false);
+    if (!t.tl || a.num_heads * (kD / kMergeDims) > kTlMaxMergeWgs) return hipErrorInvalidValue;
+    void* args[1] = {&t};
+#else
     void* args[1] = {const_cast<DecodeArgs*>(&a)};
+#endif
     return hipLaunchKernel(decode_merge_symbol(rope), dim3(a.num_heads, kD / kMergeDims),
                            dim3(64), args, 0, stream);
 }
 
 }  // namespace attn
+
+#if defined(ATTN_DECODE_TIMELINE)
+// Instrumented build only: decode calls write their timestamps to `slots`
+// records of kTlSlotWords 64-bit words at `buf` (device memory), in turn,
+// starting with record 0.  Without a buffer the decode launchers refuse.
+extern "C" int attn_timeline_set(void* buf, size_t slots) {
+    attn::tl_base = static_cast<uint64_t*>(buf);
+    attn::tl_slots = (uint32_t)slots;
+    attn::tl_next = attn::tl_cur = 0;
+    return 0;
+}
+extern "C" size_t attn_timeline_slot_words() { return attn::kTlSlotWords; }
+#endif
