@@ -73,6 +73,7 @@ int attn_set_option(const char* name, long value) {
     else if (!std::strcmp(name, "decode_splits")) which = kOptDecodeSplits;
     else if (!std::strcmp(name, "prefill_force_generic")) which = kOptPrefillForceGeneric;
     else if (!std::strcmp(name, "decode_heads_per_workgroup")) which = kOptDecodeHeadsPerGroup;
+    else if (!std::strcmp(name, "decode_kdma")) which = kOptDecodeKdma;
     else if (!std::strcmp(name, "qkv_gemm_force_generic")) which = kOptQkvGemmForceGeneric;
     else if (!std::strcmp(name, "qkv_gemm_tokens_per_wave")) which = kOptQkvGemmTokensPerWave;
     else if (!std::strcmp(name, "qkv_gemm_wide")) which = kOptQkvGemmWide;
@@ -641,7 +642,7 @@ static hipError_t replan_split_node(hipGraphExec_t graph_exec, hipGraphNode_t no
     void* args[1] = {&a};
     params.kernelParams = args;
     params.extra = nullptr;
-    params.func = const_cast<void*>(decode_split_symbol(p.path, rope));
+    params.func = const_cast<void*>(decode_split_symbol(p, rope));
     params.gridDim = decode_grid(a, p);
     return hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
 }

@@ -164,6 +164,7 @@ struct DecodePlan {
     uint32_t nstate;   // partial states per query head written to the workspace
     uint32_t block;    // threads per split workgroup
     uint32_t groups;   // KV-head groups (grid of the split workgroups: nsplit x groups)
+    uint32_t kdma;     // 1: the split kernel reads K through LDS-DMA in whole rows
 };
 
 DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_heads,
@@ -181,7 +182,7 @@ dim3 decode_grid(const DecodeArgs& a, const DecodePlan& p);  // the split kernel
 hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,
                                bool rope = false);
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream, bool rope = false);
-const void* decode_split_symbol(int path, bool rope = false);
+const void* decode_split_symbol(const DecodePlan& p, bool rope = false);
 const void* decode_merge_symbol(bool rope = false);
 int decode_path_of_symbol(const void* fn, bool rope);  // 0 when not a split kernel
 
@@ -267,7 +268,8 @@ enum Option {
     kOptPrefillStageAll = 9,      // 0 = automatic (N <= 256: all key tiles staged at once); 1 = never
     kOptPrefillSplitKeys = 10,    // 0 = automatic; 1 = never; 2 = 64-key tiles over 4 waves; 3 = 32-key units over 8 waves; 4 = 32-key units streamed per wave
     kOptPrefillKeyHalves = 11,    // 0 = automatic; 1 = never; 2 = 32-query tiles whose key tiles two 4-wave groups split
-    kOptCount = 12
+    kOptDecodeKdma = 12,          // 0 = automatic; 1 = K in registers; 2 = K through LDS-DMA
+    kOptCount = 13
 };
 long get_option(int which);
 

@@ -60,14 +60,37 @@ constexpr int kD = 128;
 constexpr int kMaxSplits = 1024;
 // longest context decoded with one KV head per workgroup (see plan_decode)
 constexpr uint32_t kOneHeadMaxKeys = 12288;
+// shortest context whose split kernel reads K through LDS-DMA (see plan_decode)
+constexpr uint32_t kDmaMinKeys = 4096;
 constexpr int kAccPitch = kD + 4;
 // cache-policy bit nt (non-temporal) of raw buffer loads
 constexpr int kNT = 2;
 
+// One 32-key batch in flight: V always in registers; K in registers in the
+// MFMA A layout (KDMA = false), or in the wave's LDS tile (KDMA = true).
+template <bool KDMA>
 struct KVBatch {
     f16x8 k[2][4];
     f16x8 v[8];
 };
+template <>
+struct KVBatch<true> {
+    f16x8 v[8];
+};
+
+// LDS-DMA of 16 bytes per lane with the non-temporal hint (see dma16)
+__device__ __forceinline__ void dma16_nt(u32x4 r, uint32_t lds, uint32_t voff) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(r)
+        : "memory");
+}
 
 template <int AUX>
 __device__ __forceinline__ float buf_ldf(BufRsrc r, uint32_t byte_off) {
@@ -105,7 +128,7 @@ __device__ __forceinline__ uint64_t tl_xcc_id() { return (uint32_t)__builtin_amd
 // each XCD then taking both halves of the same cache rows), level at 254,
 // 4096 and 16384 keys.  Longer chunks keep (nsplit, Hkv / HPW): level from
 // 40960 to 98304 keys, but 26.3-27.9 against 25.9-26.3 us at 65536.
-template <int HPW, bool ROPE>
+template <int HPW, bool ROPE, bool KDMA>
 __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     constexpr int WAVES = 8;
     constexpr int kThreads = WAVES * 64;
@@ -115,7 +138,15 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     const uint32_t c = head_groups_inner ? blockIdx.y : blockIdx.x;
     __shared__ float s_m[WAVES][16];
     __shared__ float s_l[WAVES][16];
-    __shared__ __attribute__((aligned(16))) float s_acc[WAVES][16][kAccPitch];
+    // per wave: the fold state (16 x kAccPitch floats); with KDMA it
+    // overlays the wave's two K tiles (32 rows x 256 B, one per batch in
+    // flight) that LDS-DMA fills, once the wave's last batch is consumed
+    constexpr int kWaveLds = KDMA ? 2 * 8192 : 16 * kAccPitch * 4;
+    static_assert(16 * kAccPitch * 4 <= kWaveLds);
+    __shared__ __attribute__((aligned(16))) char s_w[WAVES][kWaveLds];
+    auto sacc = [&](int w, uint32_t q) -> float* {
+        return reinterpret_cast<float*>(&s_w[w][0]) + q * kAccPitch;
+    };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -149,21 +180,40 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     // S^T row m of tile tt is key 8*(m/4) + 4*tt + (m%4) of the batch, so the
     // output of lane group gq is keys 8gq + (4tt + i).
     const uint32_t krow = 8u * (uint32_t)(n >> 2) + (uint32_t)(n & 3);
-    uint32_t koff[2], voff[8];
+    // KDMA: K is read like V, 4 whole 256-byte rows per instruction, straight
+    // into the wave's LDS tile (32 rows x 256 B): DMA instruction j, lane l
+    // loads row r = 4j + l/16, chunk (l % 16) ^ swz(r), into LDS row r, chunk
+    // l % 16, where swz(r) = (r & 3) | ((r >> 3) & 3) << 2 = l/16 | 4 (j/2).
+    // The 16 rows an A-operand read takes at one chunk then hit 16 distinct
+    // bank groups (swz(krow + 4tt) = n).  Otherwise K is loaded in the A
+    // layout directly: 16 rows x 64 B per instruction.
+    const uint32_t kq = (uint32_t)(lane >> 4);
+    uint32_t koff[2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) koff[tt] = (krow + 4u * tt) * row_bytes + 16u * gq;
+    const u32x4 rkw = rsrc_words(a.k + (uint64_t)t0 * a.kv_stride + (uint64_t)g * kD, span);
+    const uint32_t kst_base = lds_addr(&s_w[wave][0]);
+    uint32_t voff[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) voff[r] = (8u * gq + r) * row_bytes + 16u * n;
 
-    auto load = [&](uint32_t b, KVBatch& kv) {
+    auto load = [&](uint32_t b, KVBatch<KDMA>& kv, int slot) {
         const uint32_t base = b * row_bytes;
+        if constexpr (KDMA) {
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
+            for (int j = 0; j < 8; ++j)
+                dma16_nt(rkw, kst_base + 8192u * slot + 1024u * j,
+                         base + (4u * j + kq) * row_bytes +
+                             16u * (((uint32_t)lane & 15u) ^ (kq | (4u * (j >> 1)))));
+        } else {
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-                kv.k[tt][s] = __builtin_bit_cast(
-                    f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(base + koff[tt] + 64u * s),
-                                                                 0, kNT));
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    kv.k[tt][s] = __builtin_bit_cast(
+                        f16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                   rk, (int)(base + koff[tt] + 64u * s), 0, kNT));
+        }
 #pragma unroll
         for (int r = 0; r < 8; ++r)
             kv.v[r] = __builtin_bit_cast(
@@ -237,9 +287,9 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
         }
 
         // the first two batches of this wave
-        KVBatch A, B;
-        load(b, A);
-        load(b + kStep, B);
+        KVBatch<KDMA> A, B;
+        load(b, A, 0);
+        load(b + kStep, B, 1);
         TL(if (tid == 0) tl[1] = tl_now();)
 
         if constexpr (ROPE) {
@@ -254,15 +304,46 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
 
         const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
 
+        // this wave's K tile: 32 rows x 256 B in its own slice of s_acc (free
+        // until the fold), 16-byte chunk ch of row r at chunk ch ^ swz(r),
+        // swz(r) = (r & 3) | ((r >> 3) & 3) << 2, so that the 16 lanes of a
+        // row's write and the 16 rows of an A-operand read each cover all 64
+        // banks
+
         // one 32-key batch: scores, online softmax, PV
-        auto compute = [&](const KVBatch& kv, uint32_t bb) {
+        // `later`: vector memory operations this wave issued after the batch's
+        // K DMAs (its 8 V loads and the other batch's 16 when in flight)
+        auto compute = [&](const KVBatch<KDMA>& kv, int slot, uint32_t bb, bool later16) {
+            f16x8 ka[2][4];
+            if constexpr (KDMA) {
+                // the batch's K DMAs have landed: at most the vector memory
+                // operations issued after them are outstanding (its 8 V loads,
+                // and the other batch's 16 when that one is in flight)
+                if (later16)
+                    asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+                else
+                    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+                const char* const kst = &s_w[wave][8192 * slot];
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)  // row krow + 4tt has swz = n
+                        ka[tt][s] = *reinterpret_cast<const f16x8*>(
+                            kst + (krow + 4u * tt) * 256u +
+                            (((uint32_t)(4 * s + gq) ^ (uint32_t)n) << 4));
+            } else {
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) ka[tt][s] = kv.k[tt][s];
+            }
             f32x4 st[2];
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
                 st[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
-                    st[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv.k[tt][s], qb[s], st[tt], 0, 0, 0);
+                    st[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[tt][s], qb[s], st[tt], 0, 0, 0);
             }
             // scores of query n for keys bb + 8gq + r, r = 4tt + i (log2 domain)
             float x[8];
@@ -307,17 +388,18 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
         // A and let B's loads overlap A's compute.
         while (b + 2 * kStep < nk) {
             __builtin_amdgcn_sched_barrier(0);
-            compute(A, b);
-            load(b + 2 * kStep, A);
+            compute(A, 0, b, true);
+            load(b + 2 * kStep, A, 0);
             __builtin_amdgcn_sched_barrier(0);
-            compute(B, b + kStep);
-            load(b + 3 * kStep, B);
+            compute(B, 1, b + kStep, true);
+            load(b + 3 * kStep, B, 1);
             b += 2 * kStep;
         }
         __builtin_amdgcn_sched_barrier(0);
-        compute(A, b);
+        compute(A, 0, b, true);
         __builtin_amdgcn_sched_barrier(0);
-        if (b + kStep < nk) compute(B, b + kStep);  // keys past the chunk are masked (p = 0)
+        // keys past the chunk are masked (p = 0)
+        if (b + kStep < nk) compute(B, 1, b + kStep, false);
         TL(if (lane == 0) tl[2 + wave] = tl_now();)
     }
 
@@ -332,10 +414,11 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
             s_m[wave][n] = m_run;
             s_l[wave][n] = l_run;
         }
+        float* const sa = sacc(wave, n);
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s_acc[wave][n][32 * gq + 8 * i + mt] = acc[mt][i];
+            for (int i = 0; i < 4; ++i) sa[32 * gq + 8 * i + mt] = acc[mt][i];
     }
     __syncthreads();
     TL(if (tid == 0) tl[14] = tl_now();)
@@ -360,7 +443,7 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
         for (int ph = 0; ph < kPhases; ++ph) {
             const int w = hl + HPW * ph;
             const float wt = fast_exp2(s_m[w][qn] - M);  // waves without keys: 0
-            num += wt * *reinterpret_cast<const f32x4*>(&s_acc[w][qn][d]);
+            num += wt * *reinterpret_cast<const f32x4*>(sacc(w, qn) + d);
             den += wt * s_l[w][qn];
         }
         const uint32_t st = row * a.nstate + c;  // state index within the head group
@@ -461,18 +544,23 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int decode_hpw(int path) { return path == 1 ? 4 : path == 2 ? 2 : path == 3 ? 1 : 0; }
 
-// path 1/2/3: 4/2/1 KV heads per workgroup
-const void* decode_split_symbol(int path, bool rope) {
-    if (rope) {
-        if (path == 1) return reinterpret_cast<const void*>(&flash_decode_split<4, true>);
-        if (path == 2) return reinterpret_cast<const void*>(&flash_decode_split<2, true>);
-        if (path == 3) return reinterpret_cast<const void*>(&flash_decode_split<1, true>);
-        return nullptr;
-    }
-    if (path == 1) return reinterpret_cast<const void*>(&flash_decode_split<4, false>);
-    if (path == 2) return reinterpret_cast<const void*>(&flash_decode_split<2, false>);
-    if (path == 3) return reinterpret_cast<const void*>(&flash_decode_split<1, false>);
-    return generic_attention_symbol();
+template <bool ROPE, bool KDMA>
+const void* split_symbol_of(int path) {
+    if (path == 1) return reinterpret_cast<const void*>(&flash_decode_split<4, ROPE, KDMA>);
+    if (path == 2) return reinterpret_cast<const void*>(&flash_decode_split<2, ROPE, KDMA>);
+    if (path == 3) return reinterpret_cast<const void*>(&flash_decode_split<1, ROPE, KDMA>);
+    return nullptr;
+}
+
+// path 1/2/3: 4/2/1 KV heads per workgroup; kdma: K through LDS-DMA
+const void* split_symbol(int path, bool rope, bool kdma) {
+    if (rope) return kdma ? split_symbol_of<true, true>(path) : split_symbol_of<true, false>(path);
+    if (path < 1 || path > 3) return generic_attention_symbol();
+    return kdma ? split_symbol_of<false, true>(path) : split_symbol_of<false, false>(path);
+}
+
+const void* decode_split_symbol(const DecodePlan& p, bool rope) {
+    return split_symbol(p.path, rope, p.kdma != 0);
 }
 
 const void* decode_merge_symbol(bool rope) {
@@ -482,14 +570,15 @@ const void* decode_merge_symbol(bool rope) {
 
 int decode_path_of_symbol(const void* fn, bool rope) {
     for (int path = 1; path <= 3; ++path)
-        if (fn == decode_split_symbol(path, rope)) return path;
+        for (int kdma = 0; kdma < 2; ++kdma)
+            if (fn == split_symbol(path, rope, kdma != 0)) return path;
     return 0;
 }
 
 DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_heads,
                        uint32_t head_dim, uint64_t kv_stride, const void* q, const void* k,
                        const void* v, int device) {
-    DecodePlan p{0, 1, kv_len, 1, 256, 1};
+    DecodePlan p{0, 1, kv_len, 1, 256, 1, 0};
     const uint32_t G = num_heads / num_kv_heads;
     const bool mfma_ok = head_dim == kD && G >= 1 && G <= 16 && kv_stride % 8 == 0 &&
                          kv_stride * 2 <= 0x40000000ull && aligned16(q) && aligned16(k) &&
@@ -530,6 +619,11 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
     p.nsplit = nsplit;
     p.chunk = chunk;
     p.nstate = nsplit;  // one folded state per split and query head
+    // K through LDS-DMA in whole 256-byte rows once the call streams (from
+    // kDmaMinKeys keys); below, the call is latency-bound and K goes straight
+    // into registers in the MFMA layout, one step shorter per batch
+    const long kopt = get_option(kOptDecodeKdma);
+    p.kdma = kopt == 1 ? 0u : kopt == 2 ? 1u : (kv_len >= kDmaMinKeys ? 1u : 0u);
     return p;
 }
 
@@ -569,7 +663,7 @@ uint64_t* tl_record(bool next) {
 hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,
                                bool rope) {
     if (p.path < 1 || p.path > 3) return hipErrorInvalidValue;
-    const void* fn = decode_split_symbol(p.path, rope);
+    const void* fn = decode_split_symbol(p, rope);
 #if defined(ATTN_DECODE_TIMELINE)
     DecodeArgs t = a;
     t.tl = tl_record(true);

@@ -147,6 +147,30 @@ def test_decode_heads_per_workgroup(attn, gpu, hpw):
     assert_close(got, e, 2e-3, 1e-2, f"hpw={hpw}")
 
 
+@pytest.mark.parametrize("L,hpw", [(37, 1), (254, 0), (4095, 0), (20001, 2), (20001, 4),
+                                   (70001, 0)])
+def test_decode_k_paths_bitidentical(attn, gpu, L, hpw):
+    """K read through LDS-DMA in whole rows (decode_kdma=2) and K loaded into
+    registers in the MFMA layout (decode_kdma=1) feed the same values to the
+    same MFMAs: the outputs are bit-identical, and within tolerance of the
+    oracle, with sentinel rows past L and chunks ending inside a batch."""
+    q, k, v = smol_inputs(L, seed=15 + L % 7)
+    e = expected(q, k, v, L)
+    outs = {}
+    attn.set_option("decode_heads_per_workgroup", hpw)
+    try:
+        for mode in (1, 2):
+            attn.set_option("decode_kdma", mode)
+            print(f"[case] decode L={L} hpw={hpw} kdma={mode} "
+                  f"plan={attn.decode_plan(L, 16, 4, 128)}", flush=True)
+            outs[mode] = run_decode(attn, gpu, q, k, v, L, 16, 4, 128)
+    finally:
+        attn.set_option("decode_kdma", 0)
+        attn.set_option("decode_heads_per_workgroup", 0)
+    assert np.array_equal(outs[1], outs[2])
+    assert_close(outs[2], e, 2e-3, 1e-2, f"L={L} kdma")
+
+
 def test_decode_forced_generic(attn, gpu):
     L = 5000
     q, k, v = smol_inputs(L, seed=10)
