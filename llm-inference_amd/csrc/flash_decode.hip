@@ -247,6 +247,11 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
             __syncthreads();
         }
     }
+    // a chunk of at most one 32-key batch (short contexts): only the phase-0
+    // waves have keys; they store their states straight from registers and
+    // the others have nothing to do
+    const bool solo = a.chunk <= 32u;
+    if (solo && phase != 0) return;
 
     f32x4 acc[8];
 #pragma unroll
@@ -406,6 +411,35 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     // per-query sum over the four lane groups (the max is already shared)
     l_run += xor_lane(l_run, 16);
     l_run += xor_lane(l_run, 32);
+    if (solo) {
+        // the split's state is this wave's (what the fold below would give:
+        // the other waves of the head carry weight 0); lane (gq, n < G) holds
+        // dims 32gq + 8i + mt = acc[mt][i] of query n
+        if ((uint32_t)n < G) {
+            const BufRsrc rpo = make_rsrc(a.part_out, a.num_heads * a.nstate * kD * 4u);
+            const uint32_t st = (g * G + (uint32_t)n) * a.nstate + c;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t off = (st * kD + 32u * gq + 8u * i) * 4u;
+                const f32x4 lo = {acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
+                const f32x4 hi = {acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, lo), rpo,
+                                                       (int)off, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), rpo,
+                                                       (int)(off + 16u), 0, 0);
+            }
+            if (gq == 0) {
+                a.part_max[st] = m_run;
+                a.part_sum[st] = l_run;
+            }
+        }
+        TL(if (lane == 0) {
+               tl[14] = tl[10] = tl_now();
+               wait_stores();
+               tl[11] = tl_now();
+           })
+        return;
+    }
     // only the G columns that are query heads go to LDS: lane (gq, n < G)
     // holds dims 32gq .. 32gq + 31 of query n (tile mt, row 4gq + i = dim
     // 8(4gq + i) + mt), written as 16-byte rows
@@ -434,17 +468,26 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
         const uint32_t hl = row / G;
         const uint32_t qn = row - hl * G;
         const uint32_t d = (idx & 31u) * 4u;
-        float M = s_m[hl][qn];
+        // every LDS read of the item first (one round trip), then the math
+        float mw[kPhases], lw[kPhases];
+        f32x4 aw[kPhases];
 #pragma unroll
-        for (int ph = 1; ph < kPhases; ++ph) M = fmaxf(M, s_m[hl + HPW * ph][qn]);
+        for (int ph = 0; ph < kPhases; ++ph) {
+            const int w = hl + HPW * ph;
+            mw[ph] = s_m[w][qn];
+            lw[ph] = s_l[w][qn];
+            aw[ph] = *reinterpret_cast<const f32x4*>(sacc(w, qn) + d);
+        }
+        float M = mw[0];
+#pragma unroll
+        for (int ph = 1; ph < kPhases; ++ph) M = fmaxf(M, mw[ph]);
         f32x4 num = {0.f, 0.f, 0.f, 0.f};
         float den = 0.f;
 #pragma unroll
         for (int ph = 0; ph < kPhases; ++ph) {
-            const int w = hl + HPW * ph;
-            const float wt = fast_exp2(s_m[w][qn] - M);  // waves without keys: 0
-            num += wt * *reinterpret_cast<const f32x4*>(sacc(w, qn) + d);
-            den += wt * s_l[w][qn];
+            const float wt = fast_exp2(mw[ph] - M);  // waves without keys: 0
+            num += wt * aw[ph];
+            den += wt * lw[ph];
         }
         const uint32_t st = row * a.nstate + c;  // state index within the head group
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, num), rpo,
