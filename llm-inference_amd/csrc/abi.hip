@@ -9,7 +9,9 @@
 #include <atomic>
 #include <cmath>
 #include <cstring>
+#include <functional>
 #include <mutex>
+#include <unordered_map>
 
 namespace attn {
 
@@ -34,6 +36,29 @@ hipError_t captured_node(hipStream_t stream, hipGraphNode_t* out) {
 }
 
 bool fits_u32(size_t v) { return v <= 0xffffffffull; }
+
+// Partial-state count last written into each (graph exec, merge node) pair by
+// update_merge_attention_decode_node.  The merge kernel reads only the state
+// count (and buffer pointers that never change) from its arguments, so a
+// patch that keeps that count is skipped -- but only when the count also
+// equals the node's captured one: an exec node holds either its captured
+// arguments or the last ones patched in, which this table records, and a
+// stale entry (a destroyed exec's handle reused) can then only cause a
+// redundant patch, never a skipped one.  hipGraphExecKernelNodeSetParams
+// costs ~0.6 us of host time per call.
+struct MergePatchKey {
+    hipGraphExec_t exec;
+    hipGraphNode_t node;
+    bool operator==(const MergePatchKey& o) const { return exec == o.exec && node == o.node; }
+};
+struct MergePatchHash {
+    size_t operator()(const MergePatchKey& k) const {
+        return std::hash<const void*>()(k.exec) * 31u ^ std::hash<const void*>()(k.node);
+    }
+};
+std::mutex g_merge_mu;
+std::unordered_map<MergePatchKey, uint32_t, MergePatchHash> g_merge_nstate;
+constexpr size_t kMergeTableMax = 1u << 16;  // cleared when full (only costs patches)
 
 float scale_log2_for(size_t head_dim) {
     return (float)(1.4426950408889634 / std::sqrt((double)head_dim));
@@ -722,9 +747,24 @@ static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, siz
     DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(params.kernelParams[0]);
     e = hipGetDevice(&device);
     if (e != hipSuccess) return (int)e;
+    const uint32_t captured_nstate = a.nstate;
     a.kv_len = (uint32_t)kv_len;
-    return (int)(merge ? replan_merge_node(graph_exec, node, params, a, device)
-                       : replan_split_node(graph_exec, node, params, a, false, device));
+    if (!merge) return (int)replan_split_node(graph_exec, node, params, a, false, device);
+    const DecodePlan p = replan_decode(a, device);
+    if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
+    const MergePatchKey key{graph_exec, node};
+    {
+        std::lock_guard<std::mutex> lock(g_merge_mu);
+        const auto it = g_merge_nstate.find(key);
+        if (a.nstate == captured_nstate && (it == g_merge_nstate.end() || it->second == a.nstate))
+            return 0;  // the exec node already reads this many states
+    }
+    e = replan_merge_node(graph_exec, node, params, a, device);
+    if (e != hipSuccess) return (int)e;
+    std::lock_guard<std::mutex> lock(g_merge_mu);
+    if (g_merge_nstate.size() >= kMergeTableMax) g_merge_nstate.clear();
+    g_merge_nstate[key] = a.nstate;
+    return 0;
 }
 
 int attn_update_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len) {
