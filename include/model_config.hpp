@@ -17,17 +17,20 @@
 
 #pragma pack(push, 1)
 struct ModelConfig {
-    char magic[4];
-    uint32_t vocab_size;
-    uint32_t hidden_size;
-    uint32_t num_layers;
-    uint32_t num_heads;
-    uint32_t num_kv_heads;
-    uint32_t head_dim;
-    uint32_t intermediate_size;
-    uint32_t max_seq_len;
-    float rms_norm_eps;
-    float rope_theta;
+    // a default-constructed config holds the reference's defaults
+    // (model_config.hpp:14-24: 49152 vocab, 16 layers, 32 / 8 heads, eps 1e-6,
+    // theta 1); the fields the reference leaves uninitialised start at zero
+    char magic[4] = {};
+    uint32_t vocab_size = 49152;
+    uint32_t hidden_size = 0;
+    uint32_t num_layers = 16;
+    uint32_t num_heads = 32;
+    uint32_t num_kv_heads = 8;
+    uint32_t head_dim = 0;
+    uint32_t intermediate_size = 0;
+    uint32_t max_seq_len = 0;
+    float rms_norm_eps = 1e-6f;
+    float rope_theta = 1.0f;
 
     ModelConfig() = default;
 

@@ -6,10 +6,10 @@
 // file-scope device array instead of the caller's partial_out/max/sum.
 //
 // The array is per GPU and lives until the process ends.  Its device address
-// is taken once per device with hipGetSymbolAddress (the array's name is only
-// a host-side stand-in) on the first call on that device, with that device
-// current, and kept; kernels receive addresses inside it as their partial
-// state pointers.  Every call on one GPU shares the array and leaves its
+// is taken with hipGetSymbolAddress (the array's name is only a host-side
+// stand-in) on the first call on that device, with that device current, and
+// kept once that lookup has succeeded; kernels receive addresses inside it as
+// their partial state pointers.  Every call on one GPU shares the array and leaves its
 // states there; the split kernel writes every state the merge kernel reads
 // before the merge runs, so nothing needs to start at zero.  Calls that
 // overlap on one GPU (different streams without ordering) race on the array
@@ -18,6 +18,7 @@
 #include "attn_internal.hpp"
 #include "../../include/attn_mi355x.h"
 
+#include <atomic>
 #include <mutex>
 
 namespace attn {
@@ -30,23 +31,29 @@ constexpr size_t kStateFloats = 128 + 2;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
-struct ScratchSlot {
-    std::once_flag once;
-    hipError_t err = hipSuccess;
-    void* ptr = nullptr;
-};
-ScratchSlot g_slots[kMaxDevices];
+// per device: the array's address once hipGetSymbolAddress has returned it
+std::atomic<void*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
 
-// The device address of `scratch` on `device` (the current device).
+// The device address of `scratch` on `device` (the current device).  Only a
+// successful lookup is kept: a call that fails (for example one made while a
+// global-mode stream capture forbids it) returns the error and the next call
+// on that device asks again.
 hipError_t scratch_on(int device, void** ptr) {
     if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-    ScratchSlot& s = g_slots[device];
-    std::call_once(s.once, [&s] {
-        s.err = hipGetSymbolAddress(&s.ptr, HIP_SYMBOL(scratch));
-        if (s.err == hipSuccess && s.ptr == nullptr) s.err = hipErrorInvalidSymbol;
-    });
-    *ptr = s.ptr;
-    return s.err;
+    void* p = g_scratch[device].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[device].load(std::memory_order_relaxed);
+        if (!p) {
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return e;
+            if (!p) return hipErrorInvalidSymbol;
+            g_scratch[device].store(p, std::memory_order_release);
+        }
+    }
+    *ptr = p;
+    return hipSuccess;
 }
 
 }  // namespace

@@ -184,6 +184,19 @@ __global__ __launch_bounds__(512) void merge_out_proj(OutProjArgs a) {
                                         __HIP_MEMORY_SCOPE_AGENT) == H - 1u ? 1u : 0u;
     __syncthreads();
     if (s_last == 0u) return;  // workgroup-uniform
+    // Ordering of the hand-off.  The HIP memory model would need a release on
+    // the count and an acquire here; at agent scope on gfx950 those are L2
+    // write-back / invalidate operations for the whole XCD, paid once per
+    // workgroup.  Instead every partial is an agent-scope atomic store (a
+    // device-coherent store, sc1), each wave waits for its own stores to
+    // complete (s_waitcnt vmcnt(0): the store is acknowledged by the device
+    // coherence point) before the barrier and the count, and the last
+    // workgroup reads the partials with device-coherent loads (sc1, below),
+    // which do not hit stale L2 lines.  This relies on the hardware behaviour
+    // just described (completed sc1 stores are visible to sc1 loads from any
+    // XCD), not on the language model; the workgroup-scope acquire keeps the
+    // compiler from moving those loads above the count.
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     if (tid < rows) {
         // device-coherent loads (cache-policy bit sc1, as agent-scope atomic
         // loads are issued) of the heads' partials, 8 in flight, summed in

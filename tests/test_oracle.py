@@ -90,6 +90,54 @@ def test_rope_rotation_bitexact_vs_numpy_golden(golden):
         assert np.array_equal(k, x[i, 16:].reshape(-1))  # K source unchanged
 
 
+def _rotations(x, c, s):
+    """out0 = x0 c - x1 s, out1 = x1 c + x0 s (rope.hip.cpp:44-58) in fp32 with
+    every product rounded, and with either product of each output fused into
+    an FMA (evaluated exactly in fp64, rounded once to fp32): all as fp16 bits."""
+    x0, x1 = x[..., :64], x[..., 64:]
+    p = {"x0c": x0 * c, "x1s": x1 * s, "x1c": x1 * c, "x0s": x0 * s}   # fp32-rounded
+    e = {"x0c": x0.astype(np.float64) * c, "x1s": x1.astype(np.float64) * s,
+         "x1c": x1.astype(np.float64) * c, "x0s": x0.astype(np.float64) * s}
+
+    def bits(lo, hi):
+        return np.concatenate([lo.astype(np.float32).astype(np.float16),
+                               hi.astype(np.float32).astype(np.float16)], axis=-1).view(np.uint16)
+
+    plain = bits(p["x0c"] - p["x1s"], p["x1c"] + p["x0s"])
+    fused = [bits(e["x0c"] - p["x1s"], e["x1c"] + p["x0s"]),   # first product fused
+             bits(-e["x1s"] + p["x0c"], e["x0s"] + p["x1c"])]  # second product fused
+    return plain, fused
+
+
+def test_rope_contracted_rotation_is_bit_identical(golden):
+    """This build (kernels and oracle) computes rotate_pair with every product
+    rounded; the reference is compiled by hipcc with clang's default FP
+    contraction (xmake.lua:41, :80, :90 pass no -ffp-contract), which may fuse
+    a product with the subtraction/addition into one FMA.  That cannot change
+    the result: x, cos and sin are fp16 values (11 significant bits), so each
+    fp32 product has at most 22 significant bits and is exact, and
+    round(round(a c) + t) = round(a c + t).  Checked on rope.npz's inputs
+    (positions 0, 1, 2, 253, 32768, theta 5e6, 20 heads) and on a million
+    random fp16 values at random table rows up to 32768."""
+    g = golden("rope.npz")
+    x = f16(g["x"]).astype(np.float32)                    # [P, 20, 128]
+    c = f16(g["cos"]).astype(np.float32)[:, None, :]      # [P, 1, 64]
+    s = f16(g["sin"]).astype(np.float32)[:, None, :]
+    plain, fused = _rotations(x, c, s)
+    assert np.array_equal(plain, g["rotated"])            # the unfused form is the golden one
+    for f in fused:
+        assert np.array_equal(f, plain)
+    cos, sin = oracle.rope_tables(32769, 128, 5.0e6)
+    rng = np.random.default_rng(7)
+    pos = rng.integers(0, 32769, 2048)
+    c = f16(cos.reshape(32769, 64)[pos]).astype(np.float32)[:, None, :]
+    s = f16(sin.reshape(32769, 64)[pos]).astype(np.float32)[:, None, :]
+    x = (rng.standard_normal((2048, 4, 128)) * 3).astype(np.float16).astype(np.float32)
+    plain, fused = _rotations(x, c, s)
+    for f in fused:
+        assert np.array_equal(f, plain)
+
+
 def test_rope_position_zero_is_identity_and_quarter_turn_swaps():
     rng = np.random.default_rng(1)
     D, half = 128, 64

@@ -227,6 +227,26 @@ def test_cpp_headers_parse_a_file(attn, tmp_path, std):
     assert lines[5] == "size: Buffer too small for ModelConfig header (expected 44 bytes)"
 
 
+def test_cpp_model_config_defaults(tmp_path):
+    """A default-constructed ModelConfig holds the reference's defaults
+    (model_config.hpp:14-24) and zeros elsewhere; host only."""
+    src = tmp_path / "defaults.cpp"
+    src.write_text(
+        '#include "model_config.hpp"\n#include <cstdio>\n'
+        "int main() { ModelConfig c; std::printf(\"%u %u %u %u %u %u %u %u %g %g %d\\n\",\n"
+        "  c.vocab_size, c.hidden_size, c.num_layers, c.num_heads, c.num_kv_heads, c.head_dim,\n"
+        "  c.intermediate_size, c.max_seq_len, (double)c.rms_norm_eps, (double)c.rope_theta,\n"
+        "  c.magic[0] | c.magic[1] | c.magic[2] | c.magic[3]); return 0; }\n")
+    exe = tmp_path / "defaults"
+    r = subprocess.run([HIPCC, "-std=c++23", "-I", str(ROOT / "include"), str(src), "-o", str(exe),
+                        "-L", str(LIB_DIR), "-lattn_mi355x", f"-Wl,-rpath,{LIB_DIR}"],
+                       capture_output=True, text=True, timeout=180)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.split() == ["49152", "0", "16", "32", "8", "0", "0", "0", "1e-06", "1", "0"]
+
+
 @pytest.mark.parametrize("std", ["c++20", "c++23"])
 def test_engine_uses_of_model_compile(tmp_path, std):
     """The engine's uses of Model (src/main.cpp:19-30: construct from a mapped

@@ -51,10 +51,47 @@ def test_noalloc_rejects_plans_beyond_its_array(attn, gpu):
     """A plan needing more states than the array holds is rejected on the host
     before anything is enqueued: 64 query heads over 4 KV heads (the MFMA path,
     group 16) at L = 65536 need 64 x 128 states of 520 bytes, more than
-    ATTN_DECODE_NOALLOC_SCRATCH_BYTES (2 MiB).  The pointers are never
-    dereferenced (the call returns before any launch)."""
+    ATTN_DECODE_NOALLOC_SCRATCH_BYTES (2 MiB).  The call is made inside a
+    stream capture, so that even a regressed capacity check could only add
+    kernel nodes to a graph that is never launched: the graph must come back
+    empty, and the placeholder pointers are never dereferenced."""
+    import ctypes
+    from attn_mi355x import hipgraph
     lib = attn.lib()
     p = attn.decode_plan(65536, 64, 4, 128)
     assert p["path"] != 0 and 64 * p["nstate"] * 520 > (2 << 20), p
     print(f"[case] noalloc rejection plan={p}", flush=True)
-    assert lib.attn_decode_noalloc(256, 256, 256, 256, 65536, 64, 4, 128, 0, None) == 1
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    hip = hipgraph._hip
+    hip.hipGraphGetNodes.argtypes = [ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.POINTER(ctypes.c_size_t)]
+    hipgraph.begin_capture(sp)
+    rc = lib.attn_decode_noalloc(256, 256, 256, 256, 65536, 64, 4, 128, 0, sp)
+    graph = ctypes.c_void_p()
+    hipgraph.check(hip.hipStreamEndCapture(sp, ctypes.byref(graph)), "hipStreamEndCapture")
+    nodes = ctypes.c_size_t(0)
+    try:
+        hipgraph.check(hip.hipGraphGetNodes(graph, None, ctypes.byref(nodes)), "hipGraphGetNodes")
+    finally:
+        hip.hipGraphDestroy(graph)
+    assert rc == 1, rc  # hipErrorInvalidValue
+    assert nodes.value == 0
+
+
+def test_noalloc_first_call_under_global_capture(gpu):
+    """tests/cpp/test_noalloc_capture.cpp in a process of its own: the
+    process's first attn_decode_noalloc call (which also looks up the array's
+    address) made inside a hipStreamCaptureModeGlobal capture, then an eager
+    call; whichever way the lookup goes under capture, the outputs equal
+    attn_decode's bit for bit and a refused lookup is asked again."""
+    import pathlib
+    import subprocess
+    exe = pathlib.Path(__file__).resolve().parent / "cpp" / "_build" / "test_noalloc_capture"
+    assert exe.exists(), f"{exe} not built: run __graft_entry__.build()"
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    print(r.stdout)
+    print(r.stderr)
+    lines = [l for l in r.stdout.splitlines() if l.startswith(("PASS", "FAIL"))]
+    assert len(lines) >= 4, r.stdout + r.stderr
+    assert r.returncode == 0, r.stdout + r.stderr
