@@ -729,11 +729,15 @@ def decode_timeline(torch, A, hipgraph, steps=20, warmup=5):
             xcc = sp[:, 13].astype(int)
             c["wave_computed_last_per_xcd"] = {int(x): rel(wg_comp[xcc == x].max())
                                                for x in np.unique(xcc)}
+            # per wave slot of the workgroup (waves w and w + 4 share a SIMD)
+            c["wave_computed_median_per_slot"] = {
+                w: rel(float(np.median(wc[wc[:, w] > 0, w]))) for w in range(8)
+                if (wc[:, w] > 0).any()}
             calls.append(c)
         med = {}
         for k in calls[0]:
-            if k == "wave_computed_last_per_xcd":
-                med[k] = {x: float(np.median([cc[k][x] for cc in calls]))
+            if k in ("wave_computed_last_per_xcd", "wave_computed_median_per_slot"):
+                med[k] = {x: float(np.median([cc[k][x] for cc in calls if x in cc[k]]))
                           for x in calls[0][k]}
             else:
                 vals = [cc[k] for cc in calls if k in cc]
