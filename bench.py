@@ -779,9 +779,9 @@ def main():
                          "(libattn_timeline.so), plus the streaming read cold and warm")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only: the attention hot path is "
-                                   "single-device (see DESIGN.md, sharding section); run with "
-                                   "--gpus 1"}))
+        print(json.dumps({"error": "this build measures one GPU only: the attention hot path runs "
+                                   "on one device (it would shard over KV heads or context, not "
+                                   "built here); run with --gpus 1"}))
         sys.exit(2)
 
     import torch
