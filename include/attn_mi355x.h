@@ -142,7 +142,7 @@ int attn_update_rope_decode_nodes(hipGraphExec_t graph_exec, hipGraphNode_t atte
  * library-owned array of ATTN_DECODE_NOALLOC_SCRATCH_BYTES per GPU (held
  * until the process ends; its address is looked up once per device on the
  * first call there).  A plan whose states exceed the array (more than
- * ATTN_DECODE_NOALLOC_SCRATCH_BYTES / 520 query-head x split states; every
+ * ATTN_DECODE_NOALLOC_SCRATCH_BYTES / 264 query-head x split states; every
  * SmolLM3 decode shape uses at most 2048) returns hipErrorInvalidValue and
  * enqueues nothing.  Allocates nothing; not for graph capture of node handles
  * (none are returned).  Every call on one GPU shares the array: calls that

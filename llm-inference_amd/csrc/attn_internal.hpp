@@ -91,7 +91,7 @@ struct DecodeArgs {
     const f16* k;        // cache rows, kv_stride elements apart
     const f16* v;
     f16* out;            // [Hq][D] packed
-    float* part_out;     // [Hq][nstate][D]   (workspace)
+    float* part_out;     // [Hq][nstate][D] fp16 normalised outputs (workspace, see state_out)
     float* part_max;     // [Hq][nstate]      (workspace, log2 domain)
     float* part_sum;     // [Hq][nstate]      (workspace)
     uint64_t kv_stride;
@@ -140,6 +140,13 @@ constexpr uint32_t kTlMergeBase = kTlSplitWords * kTlMaxSplitWgs;
 constexpr uint32_t kTlMaxMergeWgs = 1024;
 constexpr uint32_t kTlSlotWords = kTlMergeBase + 4 * kTlMaxMergeWgs;
 #endif
+
+// The partial states' outputs: [Hq][nstate][D] fp16 at the start of the
+// caller's part_out buffer, each the state's output normalised by its own
+// sum (acc / l); the maxima and sums stay fp32 in part_max / part_sum.
+__device__ __forceinline__ f16* state_out(const DecodeArgs& a) {
+    return reinterpret_cast<f16*>(a.part_out);
+}
 
 // q head h (D = 128) rotated in place by lanes 0..7 of the calling threads
 // (lane e: pairs 8e..8e+7 and their partners 64 + 8e..), as

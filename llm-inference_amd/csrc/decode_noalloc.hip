@@ -2,7 +2,7 @@
 // that cannot allocate device memory (code under graph capture that must not
 // call hipMalloc, tight serving loops, harnesses that forbid it).  It runs the
 // same plan and kernels as attn_decode (split kernel, merge kernel); the
-// partial states (D + 2 floats per query head and split) live in a
+// partial states (D fp16 outputs and two floats per query head and split) live in a
 // file-scope device array instead of the caller's partial_out/max/sum.
 //
 // The array is per GPU and lives until the process ends.  Its device address
@@ -25,8 +25,8 @@ namespace attn {
 namespace {
 
 constexpr size_t kScratchBytes = ATTN_DECODE_NOALLOC_SCRATCH_BYTES;
-// bytes of one (query head, split) partial state: D accumulators, max, sum
-constexpr size_t kStateFloats = 128 + 2;
+// bytes of one (query head, split) partial state: D fp16 outputs, fp32 max and sum
+constexpr size_t kStateBytes = 128 * 2 + 2 * 4;
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
@@ -87,7 +87,7 @@ extern "C" int attn_decode_noalloc(const attn_f16_t* q, const attn_f16_t* k_cach
     }
     // the states of this plan must fit the array
     const size_t states = (size_t)num_heads * p.nstate;
-    if (states * kStateFloats * sizeof(float) > kScratchBytes) return (int)hipErrorInvalidValue;
+    if (states * kStateBytes > kScratchBytes) return (int)hipErrorInvalidValue;
     void* ws = nullptr;
     e = scratch_on(device, &ws);
     if (e != hipSuccess) return (int)e;
@@ -97,7 +97,7 @@ extern "C" int attn_decode_noalloc(const attn_f16_t* q, const attn_f16_t* k_cach
     a.v = reinterpret_cast<const f16*>(v_cache);
     a.out = reinterpret_cast<f16*>(out);
     a.part_out = static_cast<float*>(ws);
-    a.part_max = a.part_out + states * 128;
+    a.part_max = a.part_out + states * 64;  // after states x 128 fp16 outputs
     a.part_sum = a.part_max + states;
     a.kv_stride = kvs;
     a.kv_len = (uint32_t)kv_len;

@@ -416,17 +416,17 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
         // the other waves of the head carry weight 0); lane (gq, n < G) holds
         // dims 32gq + 8i + mt = acc[mt][i] of query n
         if ((uint32_t)n < G) {
-            const BufRsrc rpo = make_rsrc(a.part_out, a.num_heads * a.nstate * kD * 4u);
+            const BufRsrc rpo = make_rsrc(a.part_out, a.num_heads * a.nstate * kD * 2u);
             const uint32_t st = (g * G + (uint32_t)n) * a.nstate + c;
+            const float inv = 1.0f / l_run;  // l_run >= 1: the chunk's maximum has weight 1
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t off = (st * kD + 32u * gq + 8u * i) * 4u;
-                const f32x4 lo = {acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
-                const f32x4 hi = {acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, lo), rpo,
-                                                       (int)off, 0, 0);
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), rpo,
-                                                       (int)(off + 16u), 0, 0);
+                f16x8 o;
+#pragma unroll
+                for (int mt = 0; mt < 8; ++mt) o[mt] = (f16)(acc[mt][i] * inv);
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(u32x4, o), rpo, (int)((st * kD + 32u * gq + 8u * i) * 2u),
+                    0, 0);
             }
             if (gq == 0) {
                 a.part_max[st] = m_run;
@@ -461,8 +461,8 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     // idx handles 4 consecutive dims of one (head, query) state, stored with
     // one 16-byte buffer store (the range covers this workgroup's head group)
     const uint32_t rows = HPW * G;  // states of this workgroup, (head, query) order
-    const BufRsrc rpo = make_rsrc(a.part_out + (uint64_t)grp * rows * a.nstate * kD,
-                                  rows * a.nstate * kD * 4u);
+    const BufRsrc rpo = make_rsrc(state_out(a) + (uint64_t)grp * rows * a.nstate * kD,
+                                  rows * a.nstate * kD * 2u);
     for (uint32_t idx = tid; idx < rows * (kD / 4); idx += kThreads) {
         const uint32_t row = idx >> 5;  // kD / 4 = 32 items per state
         const uint32_t hl = row / G;
@@ -490,8 +490,13 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
             den += wt * lw[ph];
         }
         const uint32_t st = row * a.nstate + c;  // state index within the head group
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, num), rpo,
-                                               (int)((st * kD + d) * 4u), 0, 0);
+        // the state's output normalised by its own sum (den >= 1: the chunk's
+        // maximum has weight 1), in fp16
+        const float inv = 1.0f / den;
+        const f16x4 o = {(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv),
+                         (f16)(num[3] * inv)};
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o), rpo,
+                                              (int)((st * kD + d) * 2u), 0, 0);
         if (d == 0) {
             const uint64_t sg = (uint64_t)grp * rows * a.nstate + st;
             a.part_max[sg] = M;
@@ -527,20 +532,21 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
        })
     const BufRsrc rpm = make_rsrc(a.part_max + (uint64_t)h * S, S * 4u);
     const BufRsrc rps = make_rsrc(a.part_sum + (uint64_t)h * S, S * 4u);
-    const BufRsrc rpo = make_rsrc(a.part_out + (uint64_t)h * S * kD, S * kD * 4u);
-    const uint32_t dbyte = d0 * 4u;
+    const BufRsrc rpo = make_rsrc(state_out(a) + (uint64_t)h * S * kD, S * kD * 2u);
+    const uint32_t dbyte = d0 * 2u;
 
     float m = -INFINITY, l = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (uint32_t base = lane; base < S; base += 64u * kMergeRound) {
         float mc[kMergeRound], lc[kMergeRound];
-        f32x4 ac[kMergeRound];
+        f16x4 ac[kMergeRound];
 #pragma unroll
         for (int u = 0; u < kMergeRound; ++u) {
             const uint32_t c = base + 64u * (uint32_t)u;
             mc[u] = buf_ldf<0>(rpm, c * 4u);
             lc[u] = buf_ldf<0>(rps, c * 4u);
-            ac[u] = buf_ldf4<0>(rpo, c * (kD * 4u) + dbyte);
+            ac[u] = __builtin_bit_cast(
+                f16x4, __builtin_amdgcn_raw_buffer_load_b64(rpo, (int)(c * (kD * 2u) + dbyte), 0, 0));
         }
 #pragma unroll
         for (int u = 0; u < kMergeRound; ++u)
@@ -553,9 +559,11 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
         acc *= so;
 #pragma unroll
         for (int u = 0; u < kMergeRound; ++u) {
-            const float sc = fast_exp2(mc[u] - mn);  // invalid splits: 0
-            l += lc[u] * sc;
-            acc += ac[u] * sc;
+            // state c's weight 2^(m_c - M) l_c times its normalised output
+            const float wc = fast_exp2(mc[u] - mn) * lc[u];  // invalid splits: 0
+            l += wc;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] += (float)ac[u][e] * wc;
         }
         m = mn;
     }

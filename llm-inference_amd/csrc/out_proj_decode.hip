@@ -42,9 +42,6 @@ constexpr int kSc1 = 16;  // cache-policy bit sc1 of buffer loads: device-cohere
 __device__ __forceinline__ float ldf(BufRsrc r, uint32_t byte_off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 0));
 }
-__device__ __forceinline__ f32x2 ldf2(BufRsrc r, uint32_t byte_off) {
-    return __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)byte_off, 0, 0));
-}
 
 template <bool ROPE>
 __global__ __launch_bounds__(512) void merge_out_proj(OutProjArgs a) {
@@ -89,18 +86,20 @@ __global__ __launch_bounds__(512) void merge_out_proj(OutProjArgs a) {
     const uint32_t S = a.d.nstate;
     const BufRsrc rpm = make_rsrc(a.d.part_max + (uint64_t)h * S, S * 4u);
     const BufRsrc rps = make_rsrc(a.d.part_sum + (uint64_t)h * S, S * 4u);
-    const BufRsrc rpo = make_rsrc(a.d.part_out + (uint64_t)h * S * kDim, S * kDim * 4u);
+    const BufRsrc rpo = make_rsrc(state_out(a.d) + (uint64_t)h * S * kDim, S * kDim * 2u);
     float m = -INFINITY, l = 0.f;
     f32x2 acc = {0.f, 0.f};
     for (uint32_t base = wave; base < S; base += kWaves * kRound) {
         float mc[kRound], lc[kRound];
-        f32x2 ac[kRound];
+        f16x2 ac[kRound];
 #pragma unroll
         for (int u = 0; u < kRound; ++u) {
             const uint32_t c = base + kWaves * (uint32_t)u;  // past S: zeros
             mc[u] = ldf(rpm, c * 4u);
             lc[u] = ldf(rps, c * 4u);
-            ac[u] = ldf2(rpo, c * (kDim * 4u) + lane * 8u);
+            ac[u] = __builtin_bit_cast(
+                f16x2, __builtin_amdgcn_raw_buffer_load_b32(rpo, (int)(c * (kDim * 2u) + lane * 4u),
+                                                            0, 0));
         }
 #pragma unroll
         for (int u = 1; u < kRound; ++u)
@@ -113,9 +112,11 @@ __global__ __launch_bounds__(512) void merge_out_proj(OutProjArgs a) {
         acc *= so;
 #pragma unroll
         for (int u = 0; u < kRound; ++u) {
-            const float sc = fast_exp2(mc[u] - mn);  // invalid splits: 0
-            l += lc[u] * sc;
-            acc += ac[u] * sc;
+            // state c's weight 2^(m_c - M) l_c times its normalised output
+            const float wc = fast_exp2(mc[u] - mn) * lc[u];  // invalid splits: 0
+            l += wc;
+            acc.x += (float)ac[u][0] * wc;
+            acc.y += (float)ac[u][1] * wc;
         }
         m = mn;
     }
