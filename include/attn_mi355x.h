@@ -101,6 +101,17 @@ int attn_update_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size
  * causal_attention.hip.cpp:1003-1026). */
 int attn_update_merge_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len);
 
+/* Node records (no counterpart in the reference; a diagnostic).  Every kernel
+ * this library launches while its stream is capturing is recorded, with its
+ * launch configuration and argument as captured, until the graph holding it
+ * is released (a user object retained by that graph drops its records).  The
+ * attn_update_* functions patch a recorded node from its record; the
+ * reference updaters read every node back with hipGraphKernelNodeGetParams
+ * (causal_attention.hip.cpp:981,1009; rope.hip.cpp:215), which is what is
+ * done here for nodes without a record.  Returns the number of records
+ * held. */
+size_t attn_graph_node_records(void);
+
 /* No single counterpart in the reference: launch_rope_and_store_kv(q, k, v,
  * k_cache, v_cache, cos, sin, 1, Hq, Hkv, D, 0, 0, start_pos,
  * apply_rotation) followed by launch_causal_attention_decode(q, k_cache,
@@ -363,7 +374,9 @@ int attn_prefill_plan(const void* q, const void* k, const void* v, const void* o
  * 1025 to 4096 tokens, unless "prefill_waves" or "prefill_split_keys" is
  * set, 8-wave workgroups of 32 queries x 4 heads whose two 4-wave groups
  * take the even and the odd key tiles and combine through LDS; 1 = never;
- * 2 = at any length), "decode_out_proj_fused" (see attn_decode_out_proj).
+ * 2 = at any length), "decode_out_proj_fused" (see attn_decode_out_proj),
+ * "graph_node_records" (0 = the updaters use node records; 1 = they read
+ * every node back, as the reference does).
  * Returns 0 or -1 for an unknown name. */
 int attn_set_option(const char* name, long value);
 

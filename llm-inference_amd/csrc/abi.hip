@@ -37,13 +37,15 @@ hipError_t captured_node(hipStream_t stream, hipGraphNode_t* out) {
 
 bool fits_u32(size_t v) { return v <= 0xffffffffull; }
 
-// Partial-state count last written into each (graph exec, merge node) pair by
-// update_merge_attention_decode_node.  The merge kernel reads only the state
-// count (and buffer pointers that never change) from its arguments, so a
-// patch that keeps that count is skipped -- but only when the count also
-// equals the node's captured one: an exec node holds either its captured
-// arguments or the last ones patched in, which this table records, and a
-// stale entry (a destroyed exec's handle reused) can then only cause a
+// What a merge node's kernel reads from its arguments, last written into each
+// (graph exec, merge node) pair by update_merge_attention_decode_node or
+// update_rope_and_store_kv_decode_nodes.  The merge kernels read only the
+// state count, the rotation switch and buffer pointers that never change
+// (the fused RoPE form takes the position from the word the split kernel
+// leaves), so a patch that keeps count and switch is skipped -- but only when
+// they also equal the node's captured ones: an exec node holds either its
+// captured arguments or the last ones patched in, which this table records,
+// and a stale entry (a destroyed exec's handle reused) can then only cause a
 // redundant patch, never a skipped one.  hipGraphExecKernelNodeSetParams
 // costs ~0.6 us of host time per call.
 struct MergePatchKey {
@@ -57,8 +59,185 @@ struct MergePatchHash {
     }
 };
 std::mutex g_merge_mu;
-std::unordered_map<MergePatchKey, uint32_t, MergePatchHash> g_merge_nstate;
+std::unordered_map<MergePatchKey, uint64_t, MergePatchHash> g_merge_sig;
 constexpr size_t kMergeTableMax = 1u << 16;  // cleared when full (only costs patches)
+
+uint64_t merge_sig(const DecodeArgs& a) { return (uint64_t)a.nstate << 1 | (a.apply ? 1u : 0u); }
+
+// whether the exec node already runs the merge with `sig`, captured with
+// `captured`
+bool merge_current(hipGraphExec_t exec, hipGraphNode_t node, uint64_t captured, uint64_t sig) {
+    if (sig != captured) return false;
+    std::lock_guard<std::mutex> lock(g_merge_mu);
+    const auto it = g_merge_sig.find(MergePatchKey{exec, node});
+    return it == g_merge_sig.end() || it->second == sig;
+}
+
+void merge_patched(hipGraphExec_t exec, hipGraphNode_t node, uint64_t sig) {
+    std::lock_guard<std::mutex> lock(g_merge_mu);
+    if (g_merge_sig.size() >= kMergeTableMax) g_merge_sig.clear();
+    g_merge_sig[MergePatchKey{exec, node}] = sig;
+}
+
+// Kernel nodes remembered at capture, so that the graph updaters patch a node
+// without reading it back (hipGraphKernelNodeGetParams, ~0.07 us per call;
+// the reference updaters read the node back on every call,
+// causal_attention.hip.cpp:981,1009, rope.hip.cpp:215).  Every kernel
+// launched here while its stream is capturing is recorded with its launch
+// configuration and its one struct argument as captured, tagged with a serial
+// of the graph being captured.  The first record of a graph retains a user
+// object on that graph whose release drops the graph's records, so a node
+// handle the runtime hands out again after the graph is destroyed never meets
+// a record of the old node.  Nodes without a record (cloned graphs, a failed
+// lookup at capture, records switched off with the option
+// "graph_node_records" = 1) are read back as before.  The store is allocated
+// once and never freed, so a release during process teardown still finds it.
+constexpr size_t kNodeArgMax = 512;
+constexpr size_t kNodeRecordsMax = 1u << 16;  // cleared when full (only costs read-backs)
+struct NodeRecord {
+    uint64_t serial;
+    int device;  // the capturing stream's device
+    const void* func;
+    dim3 grid, block;
+    unsigned shmem;
+    uint32_t arg_bytes;
+    alignas(16) unsigned char arg[kNodeArgMax];
+};
+struct NodeStore {
+    std::mutex mu;
+    std::unordered_map<hipGraphNode_t, NodeRecord> nodes;
+    std::unordered_map<hipGraph_t, uint64_t> graphs;  // graphs holding a user object
+    uint64_t next_serial = 1;
+};
+NodeStore& node_store() {
+    static NodeStore* store = new NodeStore;
+    return *store;
+}
+struct GraphTag {
+    hipGraph_t graph;
+    uint64_t serial;
+};
+
+// user-object destructor: runs when the graph and its executable graphs are
+// released; it makes no HIP call
+void drop_graph_records(void* p) {
+    GraphTag* tag = static_cast<GraphTag*>(p);
+    NodeStore& s = node_store();
+    {
+        std::lock_guard<std::mutex> lock(s.mu);
+        for (auto it = s.nodes.begin(); it != s.nodes.end();)
+            it = it->second.serial == tag->serial ? s.nodes.erase(it) : std::next(it);
+        const auto g = s.graphs.find(tag->graph);
+        if (g != s.graphs.end() && g->second == tag->serial) s.graphs.erase(g);
+    }
+    delete tag;
+}
+
+// The serial of a graph under capture, retaining the user object the first
+// time; 0 when the runtime refuses it (then nothing is recorded).
+uint64_t graph_serial(hipGraph_t graph) {
+    NodeStore& s = node_store();
+    uint64_t serial = 0;
+    {
+        std::lock_guard<std::mutex> lock(s.mu);
+        const auto it = s.graphs.find(graph);
+        if (it != s.graphs.end()) return it->second;
+        serial = s.next_serial++;
+    }
+    GraphTag* tag = new GraphTag{graph, serial};
+    hipUserObject_t obj = nullptr;
+    if (hipUserObjectCreate(&obj, tag, drop_graph_records, 1, hipUserObjectNoDestructorSync) !=
+        hipSuccess) {
+        delete tag;
+        return 0;
+    }
+    if (hipGraphRetainUserObject(graph, obj, 1, hipGraphUserObjectMove) != hipSuccess) {
+        (void)hipUserObjectRelease(obj, 1);  // runs drop_graph_records, which frees tag
+        return 0;
+    }
+    std::lock_guard<std::mutex> lock(s.mu);
+    return s.graphs.emplace(graph, serial).first->second;
+}
+
+// After a launch on `stream`: if the stream is capturing, record the node the
+// launch added.  Args is the kernel's one struct argument.
+template <class Args>
+void remember_launch(hipStream_t stream) {
+    static_assert(sizeof(Args) <= kNodeArgMax, "node argument larger than a record");
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    hipGraph_t graph = nullptr;
+    const hipGraphNode_t* deps = nullptr;
+    size_t count = 0;
+    if (hipStreamGetCaptureInfo_v2(stream, &status, nullptr, &graph, &deps, &count) !=
+            hipSuccess ||
+        status != hipStreamCaptureStatusActive || count != 1 || !deps || !graph)
+        return;
+    const hipGraphNode_t node = deps[0];
+    hipKernelNodeParams p{};
+    if (hipGraphKernelNodeGetParams(node, &p) != hipSuccess || !p.kernelParams || !p.func) return;
+    hipDevice_t device = 0;
+    if (hipStreamGetDevice(stream, &device) != hipSuccess) return;
+    NodeRecord r;
+    r.device = (int)device;
+    r.func = p.func;
+    r.grid = p.gridDim;
+    r.block = p.blockDim;
+    r.shmem = p.sharedMemBytes;
+    r.arg_bytes = (uint32_t)sizeof(Args);
+    std::memcpy(r.arg, p.kernelParams[0], sizeof(Args));
+    r.serial = graph_serial(graph);
+    if (r.serial == 0) return;
+    NodeStore& s = node_store();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (s.nodes.size() >= kNodeRecordsMax) s.nodes.clear();
+    s.nodes[node] = r;
+}
+
+// A kernel node as an updater sees it: launch configuration and a pointer to
+// its one struct argument (a private copy, or the node's own storage when it
+// had to be read back).
+struct NodeView {
+    hipKernelNodeParams params{};
+    const void* arg = nullptr;
+    int device = -1;  // recorded nodes: the device they were captured on
+    alignas(16) unsigned char copy[kNodeArgMax];
+};
+
+hipError_t view_node(hipGraphNode_t node, NodeView& v) {
+    if (get_option(kOptGraphNodeRecords) != 1) {
+        NodeStore& s = node_store();
+        std::lock_guard<std::mutex> lock(s.mu);
+        const auto it = s.nodes.find(node);
+        if (it != s.nodes.end()) {
+            const NodeRecord& r = it->second;
+            v.params = hipKernelNodeParams{};
+            v.params.func = const_cast<void*>(r.func);
+            v.params.gridDim = r.grid;
+            v.params.blockDim = r.block;
+            v.params.sharedMemBytes = r.shmem;
+            std::memcpy(v.copy, r.arg, r.arg_bytes);
+            v.arg = v.copy;
+            v.device = r.device;
+            return hipSuccess;
+        }
+    }
+    v.params = hipKernelNodeParams{};
+    const hipError_t e = hipGraphKernelNodeGetParams(node, &v.params);
+    if (e != hipSuccess) return e;
+    if (!v.params.kernelParams) return hipErrorInvalidValue;
+    v.arg = v.params.kernelParams[0];
+    return hipSuccess;
+}
+
+// The device a node's plan is made for: its capturing stream's when recorded,
+// else the current one.
+hipError_t node_device(const NodeView& v, int* device) {
+    if (v.device >= 0) {
+        *device = v.device;
+        return hipSuccess;
+    }
+    return hipGetDevice(device);
+}
 
 float scale_log2_for(size_t head_dim) {
     return (float)(1.4426950408889634 / std::sqrt((double)head_dim));
@@ -99,6 +278,7 @@ int attn_set_option(const char* name, long value) {
     else if (!std::strcmp(name, "prefill_force_generic")) which = kOptPrefillForceGeneric;
     else if (!std::strcmp(name, "decode_heads_per_workgroup")) which = kOptDecodeHeadsPerGroup;
     else if (!std::strcmp(name, "decode_kdma")) which = kOptDecodeKdma;
+    else if (!std::strcmp(name, "graph_node_records")) which = kOptGraphNodeRecords;
     else if (!std::strcmp(name, "qkv_gemm_force_generic")) which = kOptQkvGemmForceGeneric;
     else if (!std::strcmp(name, "qkv_gemm_tokens_per_wave")) which = kOptQkvGemmTokensPerWave;
     else if (!std::strcmp(name, "qkv_gemm_wide")) which = kOptQkvGemmWide;
@@ -110,6 +290,12 @@ int attn_set_option(const char* name, long value) {
     if (which < 0) return -1;
     g_options[which].store(value, std::memory_order_relaxed);
     return 0;
+}
+
+size_t attn_graph_node_records(void) {
+    NodeStore& s = node_store();
+    std::lock_guard<std::mutex> lock(s.mu);
+    return s.nodes.size();
 }
 
 size_t attn_decode_workspace_states(size_t num_heads, size_t kv_len) {
@@ -165,7 +351,9 @@ int attn_rope_store_kv(attn_f16_t* q, attn_f16_t* k, const attn_f16_t* v,
     a.apply = apply_rotation ? 1u : 0u;
     a.lanes_per_head = (uint32_t)(head_dim / 16);
     const bool vec = rope_vector_ok(a);
-    return (int)launch_rope_kernel(a, vec, stream);
+    const hipError_t e = launch_rope_kernel(a, vec, stream);
+    if (e == hipSuccess) remember_launch<RopeArgs>(stream);
+    return (int)e;
 }
 
 int attn_rope(attn_f16_t* q, attn_f16_t* k, const attn_f16_t* cos_table,
@@ -179,12 +367,13 @@ int attn_rope(attn_f16_t* q, attn_f16_t* k, const attn_f16_t* cos_table,
 
 int attn_update_rope_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t start_pos,
                           int apply_rotation) {
-    hipKernelNodeParams params{};
-    hipError_t e = hipGraphKernelNodeGetParams(node, &params);
+    NodeView view;
+    hipError_t e = view_node(node, view);
     if (e != hipSuccess) return (int)e;
+    hipKernelNodeParams& params = view.params;
     if (params.func != rope_kernel_symbol(true) && params.func != rope_kernel_symbol(false))
         return (int)hipErrorInvalidValue;
-    RopeArgs a = *reinterpret_cast<const RopeArgs*>(params.kernelParams[0]);
+    RopeArgs a = *reinterpret_cast<const RopeArgs*>(view.arg);
     if (!fits_u32(start_pos + a.seq_len)) return (int)hipErrorInvalidValue;
     if (!apply_rotation && a.kc == nullptr) return (int)hipErrorInvalidValue;
     a.start_pos = (uint32_t)start_pos;
@@ -241,18 +430,21 @@ int attn_qkv_rope_store_kv_decode(const attn_f16_t* x, attn_f16_t* y, const attn
     a.head_dim = (uint32_t)head_dim;
     a.start_pos = (uint32_t)start_pos;
     a.apply = apply_rotation ? 1u : 0u;
-    return (int)launch_qkv_kernel(a, true, stream);
+    const hipError_t e = launch_qkv_kernel(a, true, stream);
+    if (e == hipSuccess) remember_launch<QkvArgs>(stream);
+    return (int)e;
 }
 
 int attn_update_qkv_rope_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t start_pos,
                               int apply_rotation) {
-    hipKernelNodeParams params{};
-    hipError_t e = hipGraphKernelNodeGetParams(node, &params);
+    NodeView view;
+    hipError_t e = view_node(node, view);
     if (e != hipSuccess) return (int)e;
+    hipKernelNodeParams& params = view.params;
     if (params.func != qkv_kernel_symbol(true, true) && params.func != qkv_kernel_symbol(true, false))
         return (int)hipErrorInvalidValue;
     if (!fits_u32(start_pos)) return (int)hipErrorInvalidValue;
-    QkvArgs a = *reinterpret_cast<const QkvArgs*>(params.kernelParams[0]);
+    QkvArgs a = *reinterpret_cast<const QkvArgs*>(view.arg);
     a.start_pos = (uint32_t)start_pos;
     a.apply = apply_rotation ? 1u : 0u;
     void* args[1] = {&a};
@@ -422,12 +614,14 @@ static int enqueue_decode(DecodeArgs& a, int device, bool rope, hipStream_t stre
     if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
     hipError_t e = launch_decode_split(a, p, stream, rope);
     if (e != hipSuccess) return (int)e;
+    remember_launch<DecodeArgs>(stream);
     if (attention_node) {
         e = captured_node(stream, attention_node);
         if (e != hipSuccess) return (int)e;
     }
     e = launch_decode_merge(a, stream, rope);
     if (e != hipSuccess) return (int)e;
+    remember_launch<DecodeArgs>(stream);
     if (merge_node) {
         e = captured_node(stream, merge_node);
         if (e != hipSuccess) return (int)e;
@@ -473,6 +667,7 @@ int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t
         g.scale_log2 = scale_log2_for(head_dim);
         e = launch_generic_attention(g, stream);
         if (e != hipSuccess) return (int)e;
+        remember_launch<GenericAttnArgs>(stream);
         if (attention_node || merge_node) {
             hipGraphNode_t node = nullptr;
             e = captured_node(stream, &node);
@@ -644,12 +839,14 @@ int attn_decode_out_proj(const attn_f16_t* q, const attn_f16_t* k_cache, const a
     if (p.path < 1 || p.path > 3 || !out_proj_fused_ok(o)) return two_launches();
     e = launch_decode_split(a, p, stream, false);
     if (e != hipSuccess) return (int)e;
+    remember_launch<DecodeArgs>(stream);
     if (attention_node) {
         e = captured_node(stream, attention_node);
         if (e != hipSuccess) return (int)e;
     }
     e = launch_merge_out_proj(o, stream, false);
     if (e != hipSuccess) return (int)e;
+    remember_launch<OutProjArgs>(stream);
     if (merge_node) {
         e = captured_node(stream, merge_node);
         if (e != hipSuccess) return (int)e;
@@ -687,25 +884,35 @@ int attn_update_rope_decode_nodes(hipGraphExec_t graph_exec, hipGraphNode_t atte
                                   hipGraphNode_t merge_node, size_t kv_len, size_t start_pos,
                                   int apply_rotation) {
     if (kv_len == 0 || !fits_u32(kv_len) || start_pos >= kv_len) return (int)hipErrorInvalidValue;
-    int device = 0;
-    hipError_t e = hipGetDevice(&device);
-    if (e != hipSuccess) return (int)e;
     for (int m = 0; m < 2; ++m) {
         hipGraphNode_t node = m ? merge_node : attention_node;
-        hipKernelNodeParams params{};
-        e = hipGraphKernelNodeGetParams(node, &params);
+        NodeView view;
+        hipError_t e = view_node(node, view);
         if (e != hipSuccess) return (int)e;
+        int device = 0;
+        e = node_device(view, &device);
+        if (e != hipSuccess) return (int)e;
+        hipKernelNodeParams& params = view.params;
         const bool ok = m ? params.func == decode_merge_symbol(true)
                           : decode_path_of_symbol(params.func, true) != 0;
         if (!ok) return (int)hipErrorInvalidValue;
-        DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(params.kernelParams[0]);
+        DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(view.arg);
+        const uint64_t captured = merge_sig(a);
         a.kv_len = (uint32_t)kv_len;
         a.row = (uint32_t)start_pos;
         a.apply = apply_rotation ? 1u : 0u;
         if (a.apply && (!a.cos_t || !a.sin_t)) return (int)hipErrorInvalidValue;
-        e = m ? replan_merge_node(graph_exec, node, params, a, device)
-              : replan_split_node(graph_exec, node, params, a, true, device);
+        if (!m) {
+            e = replan_split_node(graph_exec, node, params, a, true, device);
+            if (e != hipSuccess) return (int)e;
+            continue;
+        }
+        const DecodePlan p = replan_decode(a, device);
+        if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
+        if (merge_current(graph_exec, node, captured, merge_sig(a))) continue;
+        e = replan_merge_node(graph_exec, node, params, a, device);
         if (e != hipSuccess) return (int)e;
+        merge_patched(graph_exec, node, merge_sig(a));
     }
     return 0;
 }
@@ -713,12 +920,13 @@ int attn_update_rope_decode_nodes(hipGraphExec_t graph_exec, hipGraphNode_t atte
 static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, size_t kv_len,
                              bool merge) {
     if (kv_len == 0 || !fits_u32(kv_len)) return (int)hipErrorInvalidValue;
-    hipKernelNodeParams params{};
-    hipError_t e = hipGraphKernelNodeGetParams(node, &params);
+    NodeView view;
+    hipError_t e = view_node(node, view);
     if (e != hipSuccess) return (int)e;
+    hipKernelNodeParams& params = view.params;
     if (params.func == generic_attention_symbol()) {
         if (merge) return 0;  // single-kernel path: nothing separate to patch
-        GenericAttnArgs g = *reinterpret_cast<const GenericAttnArgs*>(params.kernelParams[0]);
+        GenericAttnArgs g = *reinterpret_cast<const GenericAttnArgs*>(view.arg);
         if (g.causal) return (int)hipErrorInvalidValue;  // a prefill node, not decode
         g.kv_len = (uint32_t)kv_len;
         void* args[1] = {&g};
@@ -730,8 +938,8 @@ static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, siz
     if (params.func == merge_out_proj_symbol(false)) {
         // the merge fused into o_proj: its decode arguments follow kv_len
         if (!merge) return (int)hipErrorInvalidValue;
-        OutProjArgs o = *reinterpret_cast<const OutProjArgs*>(params.kernelParams[0]);
-        e = hipGetDevice(&device);
+        OutProjArgs o = *reinterpret_cast<const OutProjArgs*>(view.arg);
+        e = node_device(view, &device);
         if (e != hipSuccess) return (int)e;
         o.d.kv_len = (uint32_t)kv_len;
         const DecodePlan p = replan_decode(o.d, device);
@@ -744,26 +952,19 @@ static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, siz
     const bool is_split = decode_path_of_symbol(params.func, false) != 0;
     const bool is_merge = params.func == decode_merge_symbol();
     if ((merge && !is_merge) || (!merge && !is_split)) return (int)hipErrorInvalidValue;
-    DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(params.kernelParams[0]);
-    e = hipGetDevice(&device);
+    DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(view.arg);
+    e = node_device(view, &device);
     if (e != hipSuccess) return (int)e;
-    const uint32_t captured_nstate = a.nstate;
+    const uint64_t captured = merge_sig(a);
     a.kv_len = (uint32_t)kv_len;
     if (!merge) return (int)replan_split_node(graph_exec, node, params, a, false, device);
     const DecodePlan p = replan_decode(a, device);
     if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
-    const MergePatchKey key{graph_exec, node};
-    {
-        std::lock_guard<std::mutex> lock(g_merge_mu);
-        const auto it = g_merge_nstate.find(key);
-        if (a.nstate == captured_nstate && (it == g_merge_nstate.end() || it->second == a.nstate))
-            return 0;  // the exec node already reads this many states
-    }
+    // the exec node already reads this many states
+    if (merge_current(graph_exec, node, captured, merge_sig(a))) return 0;
     e = replan_merge_node(graph_exec, node, params, a, device);
     if (e != hipSuccess) return (int)e;
-    std::lock_guard<std::mutex> lock(g_merge_mu);
-    if (g_merge_nstate.size() >= kMergeTableMax) g_merge_nstate.clear();
-    g_merge_nstate[key] = a.nstate;
+    merge_patched(graph_exec, node, merge_sig(a));
     return 0;
 }
 

@@ -148,16 +148,27 @@ __device__ __forceinline__ f16* state_out(const DecodeArgs& a) {
     return reinterpret_cast<f16*>(a.part_out);
 }
 
-// q head h (D = 128) rotated in place by lanes 0..7 of the calling threads
-// (lane e: pairs 8e..8e+7 and their partners 64 + 8e..), as
+// The fused RoPE + decode form: the split kernel leaves the new token's
+// position in the word after the fp16 partial outputs, and the merge kernel
+// that rotates q reads it there, so a merge node whose state count and
+// rotation switch are unchanged needs no patch when the position moves.  The
+// caller's partial_out holds at least num_heads * nstate * D floats, twice
+// the fp16 outputs, so the word lies inside it.
+__device__ __forceinline__ uint32_t* rope_row_word(const DecodeArgs& a) {
+    return reinterpret_cast<uint32_t*>(state_out(a) + (uint64_t)a.num_heads * a.nstate * 128u);
+}
+
+// q head h (D = 128) at position `row` rotated in place by lanes 0..7 of the
+// calling threads (lane e: pairs 8e..8e+7 and their partners 64 + 8e..), as
 // launch_rope_and_store_kv leaves it; used by the merge kernels of the fused
 // RoPE + decode form once every split workgroup has read q.
-__device__ __forceinline__ void rotate_q_head(const DecodeArgs& a, uint32_t h, uint32_t e) {
+__device__ __forceinline__ void rotate_q_head(const DecodeArgs& a, uint32_t h, uint32_t e,
+                                              uint32_t row) {
     const uint32_t c8 = 8u * e;
     f16* qh = a.q_rot + (uint64_t)h * 128u;
     f16x8 x0 = ld16(qh + c8), x1 = ld16(qh + 64 + c8);
-    rope_rotate8(x0, x1, ld16(a.cos_t + (uint64_t)a.row * 64u + c8),
-                 ld16(a.sin_t + (uint64_t)a.row * 64u + c8), x0, x1);
+    rope_rotate8(x0, x1, ld16(a.cos_t + (uint64_t)row * 64u + c8),
+                 ld16(a.sin_t + (uint64_t)row * 64u + c8), x0, x1);
     st16(qh + c8, x0);
     st16(qh + 64 + c8, x1);
 }
@@ -276,7 +287,8 @@ enum Option {
     kOptPrefillSplitKeys = 10,    // 0 = automatic; 1 = never; 2 = 64-key tiles over 4 waves; 3 = 32-key units over 8 waves; 4 = 32-key units streamed per wave
     kOptPrefillKeyHalves = 11,    // 0 = automatic; 1 = never; 2 = 32-query tiles whose key tiles two 4-wave groups split
     kOptDecodeKdma = 12,          // 0 = automatic; 1 = K in registers; 2 = K through LDS-DMA
-    kOptCount = 13
+    kOptGraphNodeRecords = 13,    // 0 = updaters use the nodes recorded at capture; 1 = read nodes back
+    kOptCount = 14
 };
 long get_option(int which);
 

@@ -243,6 +243,10 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
                     st16(a.v_dst + dst + c16 + 8, ld16(a.v_src + src + c16 + 8));
                 }
             }
+            // the position, for the merge kernel's rotation of q
+            if (grp == 0 && hw == 0 && phase == 0 && lane == 16)
+                __builtin_amdgcn_raw_buffer_store_b32(a.row, make_rsrc(rope_row_word(a), 4u), 0,
+                                                      0, 0);
             wait_stores();
             __syncthreads();
         }
@@ -534,6 +538,10 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
     const BufRsrc rps = make_rsrc(a.part_sum + (uint64_t)h * S, S * 4u);
     const BufRsrc rpo = make_rsrc(state_out(a) + (uint64_t)h * S * kD, S * kD * 2u);
     const uint32_t dbyte = d0 * 2u;
+    // the rotating lanes fetch the position first, alongside the states
+    const bool rotates = ROPE && a.apply && blockIdx.y < 8 && lane == 0;
+    uint32_t row = 0;
+    if (rotates) row = __hip_atomic_load(rope_row_word(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
     float m = -INFINITY, l = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -585,7 +593,7 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
     TL(wait_stores(); if (lane == 0) tl[2] = tl_now();)
     if constexpr (ROPE) {
         // every split workgroup has read q (the kernel boundary orders this)
-        if (a.apply && blockIdx.y < 8 && lane == 0) rotate_q_head(a, h, blockIdx.y);
+        if (rotates) rotate_q_head(a, h, blockIdx.y, row);
     }
 }
 

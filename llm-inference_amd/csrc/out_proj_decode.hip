@@ -145,7 +145,7 @@ __global__ __launch_bounds__(512) void merge_out_proj(OutProjArgs a) {
     }
     if constexpr (ROPE) {
         // every split workgroup has read q (the kernel boundary orders this)
-        if (rb == 0 && a.d.apply && tid < 8u) rotate_q_head(a.d, h, tid);
+        if (rb == 0 && a.d.apply && tid < 8u) rotate_q_head(a.d, h, tid, a.d.row);
     }
     __syncthreads();
 

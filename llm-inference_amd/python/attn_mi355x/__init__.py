@@ -93,6 +93,7 @@ def _declare(lib):
         "attn_weights_layout_for": (_c.c_int, [_c.POINTER(ModelConfigC), _c.c_uint64,
                                                _c.POINTER(WeightsLayout)]),
         "attn_weights_error_string": (_c.c_char_p, [_c.c_int]),
+        "attn_graph_node_records": (_sz, []),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -122,7 +123,7 @@ def exported_symbols():
             "attn_update_rope_decode_nodes", "attn_weights_parse", "attn_weights_layout_for",
             "attn_decode_noalloc", "attn_out_proj_decode",
             "attn_decode_out_proj_workspace_bytes", "attn_decode_out_proj",
-            "attn_weights_error_string"]
+            "attn_weights_error_string", "attn_graph_node_records"]
 
 
 def _ptr(x) -> Optional[int]:

@@ -259,6 +259,88 @@ def test_decode_graph_node_update(attn, gpu):
         hipgraph.destroy(graph, exe)
 
 
+def test_graph_node_records(attn, gpu):
+    """The updaters patch nodes from the records made at capture: a RoPE /
+    append node and a decode pair captured into one graph are recorded (three
+    records), patches from the records and patches that read every node back
+    (option graph_node_records = 1, the reference's way) give bit-identical
+    replays, equal to eager launches, and the records are dropped when the
+    graph and its executable graph are destroyed."""
+    import ctypes
+    import time
+
+    from attn_mi355x import hipgraph
+    lib = attn.lib()
+    Lmax = 9000
+    q, k, v = smol_inputs(Lmax, seed=17)
+    rng = np.random.default_rng(17)
+    kn = rng.standard_normal(512).astype(np.float16).view(np.uint16)
+    vn = rng.standard_normal(512).astype(np.float16).view(np.uint16)
+    cos, sin = attn.rope_tables(Lmax, 128, 5e4)
+    dcos, dsin = cos.reshape(-1).to(gpu), sin.reshape(-1).to(gpu)
+    dq0, dk, dv = dev(q, gpu), dev(k, gpu), dev(v, gpu)
+    dkn, dvn = dev(kn, gpu), dev(vn, gpu)
+    states = attn.decode_workspace_states(16, Lmax)
+    po, pm, ps = (torch.empty(states * 128, device=gpu), torch.empty(states, device=gpu),
+                  torch.empty(states, device=gpu))
+    dq = dq0.clone()
+    out_g = torch.empty(2048, dtype=torch.float16, device=gpu)
+    before = lib.attn_graph_node_records()
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    anode, mnode = ctypes.c_void_p(), ctypes.c_void_p()
+    L0 = 300
+    with torch.cuda.stream(stream):
+        hipgraph.begin_capture(sp)
+        assert lib.attn_rope_store_kv(dq.data_ptr(), dkn.data_ptr(), dvn.data_ptr(), dk.data_ptr(),
+                                      dv.data_ptr(), dcos.data_ptr(), dsin.data_ptr(), 1, 16, 4,
+                                      128, 0, 0, L0 - 1, 1, sp) == 0
+        rnode = hipgraph.last_captured_node(sp)
+        assert lib.attn_decode(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), out_g.data_ptr(),
+                               po.data_ptr(), pm.data_ptr(), ps.data_ptr(), 1, L0, L0 - 1, 16, 4,
+                               128, 0, 0, sp, ctypes.byref(anode), ctypes.byref(mnode)) == 0
+        graph, exe = hipgraph.end_capture(sp)
+    destroyed = False
+    try:
+        assert lib.attn_graph_node_records() == before + 3
+        outs = {}
+        for rec in (0, 1):
+            attn.set_option("graph_node_records", rec)
+            try:
+                for L in (L0, 301, 4096, 8999, 301):
+                    assert lib.attn_update_rope_node(exe, rnode, L - 1, 1) == 0
+                    assert lib.attn_update_decode_node(exe, anode, L) == 0
+                    assert lib.attn_update_merge_node(exe, mnode, L) == 0
+                    dq.copy_(dq0)
+                    torch.cuda.synchronize()
+                    hipgraph.launch(exe, sp)
+                    hipgraph.synchronize(sp)
+                    print(f"[case] node records={rec} L={L}", flush=True)
+                    outs.setdefault(L, []).append(host(out_g))
+            finally:
+                attn.set_option("graph_node_records", 0)
+        for L, (a, b, *rest) in outs.items():
+            assert np.array_equal(a, b), L
+            for c in rest:
+                assert np.array_equal(a, c), L
+        # eager equivalent of the last replay (L = 301)
+        dq.copy_(dq0)
+        out_e = torch.empty(2048, dtype=torch.float16, device=gpu)
+        attn.rope_store_kv(dq, dkn, dvn, dk, dv, dcos, dsin, 1, 16, 4, 128, 0, 0, 300, True)
+        attn.decode(dq, dk, dv, out_e, po, pm, ps, 1, 301, 300, 16, 4, 128, 0, 0)
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out_e), outs[301][-1])
+        hipgraph.destroy(graph, exe)
+        destroyed = True
+        deadline = time.monotonic() + 5.0
+        while lib.attn_graph_node_records() != before and time.monotonic() < deadline:
+            time.sleep(0.01)
+        assert lib.attn_graph_node_records() == before
+    finally:
+        if not destroyed:
+            hipgraph.destroy(graph, exe)
+
+
 @pytest.mark.parametrize("Hq,Hkv,hpw,L0", [(16, 2, 0, 50), (8, 1, 0, 50), (16, 4, 4, 50),
                                           (16, 4, 0, 19999)])
 def test_decode_graph_node_update_other_paths(attn, gpu, Hq, Hkv, hpw, L0):

@@ -116,7 +116,10 @@ def test_fused_graph_replays_with_node_updates(attn, gpu):
     """Capture once, then per step patch kv_len / start_pos / apply_rotation
     with attn_update_rope_decode_nodes and replay; q is restored from a
     pristine copy between steps (the engine projects a fresh one).  Every
-    replay equals an eager fused call on identical buffers bit for bit."""
+    replay equals an eager fused call on identical buffers bit for bit.
+    Consecutive positions with the same state count and rotation switch
+    leave the merge node unpatched (it reads the position the split kernel
+    leaves in the workspace), so q must still be rotated at the new one."""
     from attn_mi355x import hipgraph
     Lmax = 40001
     q, k, v, cache, cos, sin, S = inputs(Lmax, Lmax - 1, seed=77)
@@ -132,6 +135,7 @@ def test_fused_graph_replays_with_node_updates(attn, gpu):
         graph, exe = hipgraph.end_capture(sp)
     try:
         for L, apply in ((100, True), (101, False), (254, True), (4097, True), (33000, False),
+                         (33001, False), (33002, True), (33003, True), (33004, True),
                          (40001, True), (100, True)):
             assert attn.lib().attn_update_rope_decode_nodes(exe, nodes[0], nodes[1], L, L - 1,
                                                             1 if apply else 0) == 0
