@@ -684,6 +684,7 @@ def decode_timeline(torch, A, hipgraph, steps=20, warmup=5):
         plan = A.decode_plan(L, HQ, HKV, D, KV_DIM)
         groups = HKV // {1: 4, 2: 2, 3: 1}[plan["path"]]
         nsplit_wg = groups * plan["nsplit"]
+        whole = plan["nsplit"] == 1  # one kernel: no merge records
         nmerge = HQ * (D // 4)
         buf.zero_()
         torch.cuda.synchronize()
@@ -717,12 +718,15 @@ def decode_timeline(torch, A, hipgraph, steps=20, warmup=5):
                 "last_wg_computed": rel(wg_comp[last_wg]),
                 "last_wg_barrier": rel(sp[last_wg, 14]),
                 "last_wg_fold": rel(sp[last_wg, 10]),
-                "merge_entry_first": rel(mg[:, 0].min()),
-                "merge_entry_last": rel(mg[:, 0].max()),
-                "merge_states_folded_median": rel(np.median(mg[:, 1])),
-                "merge_states_folded_last": rel(mg[:, 1].max()),
-                "merge_stored_last": rel(mg[:, 2].max()),
             }
+            if not whole:
+                c.update({
+                    "merge_entry_first": rel(mg[:, 0].min()),
+                    "merge_entry_last": rel(mg[:, 0].max()),
+                    "merge_states_folded_median": rel(np.median(mg[:, 1])),
+                    "merge_states_folded_last": rel(mg[:, 1].max()),
+                    "merge_stored_last": rel(mg[:, 2].max()),
+                })
             if s + 1 < warmup + steps:
                 nxt = rec[s + 1][:split_words * nsplit_wg].reshape(nsplit_wg, split_words)
                 c["next_call_split_entry"] = rel(float(nxt[:, 0].min()))

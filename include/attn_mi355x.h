@@ -78,8 +78,11 @@ int attn_prefill(const attn_f16_t* q, const attn_f16_t* k, const attn_f16_t* v,
  * floats); their contents are private to this library and nothing past that
  * capacity is written.  For head_dim 128 two kernels are enqueued, the split
  * kernel (*attention_node) and the partial merge (*merge_node), as in the
- * reference; other shapes enqueue one generic kernel and both handles
- * receive it.
+ * reference; up to 384 keys the split kernel alone when merge_node is NULL
+ * (one workgroup per KV head writes the output; with merge_node the merge
+ * kernel follows and exits at once, so that an updater can move the pair to
+ * a longer context); other shapes enqueue one generic kernel and both
+ * handles receive it.
  * Replaces launch_causal_attention_decode (kernels.hpp:104-123) and
  * launch_causal_attention_decode_vectorized (kernels.hpp:127-146;
  * causal_attention.hip.cpp:840-972). */
@@ -222,8 +225,10 @@ int attn_out_proj_decode(const attn_f16_t* x, attn_f16_t* y, const attn_f16_t* w
  * the pair within fp32 rounding of the partial sums (heads summed in order;
  * deterministic).  The fused form is measured slower on MI355X (its cross-XCD
  * reduction of the heads costs more than the kernel boundary it removes) and
- * stays selectable for that measurement.  Other shapes, or a null workspace,
- * always issue the two launches.  out_proj_workspace:
+ * stays selectable for that measurement; it splits every context (no
+ * one-kernel decode of short contexts, see "decode_whole_max_keys").  Other
+ * shapes, or a null workspace, always issue the two launches.
+ * out_proj_workspace:
  * attn_decode_out_proj_workspace_bytes(Hq, hidden_size) bytes, 256-byte
  * aligned, ZERO-FILLED once before the first call; every call leaves its
  * counters zero again.  Calls sharing a workspace must be ordered (one
@@ -354,9 +359,10 @@ int attn_prefill_plan(const void* q, const void* k, const void* v, const void* o
  * "decode_force_generic", "decode_splits" (0 = automatic),
  * "decode_heads_per_workgroup" (0 = automatic: 1 up to 12288 keys, 2 above
  * when Hkv is even; 1, 2 or 4 KV heads per split workgroup, reduced to what
- * Hkv allows), "decode_kdma" (0 = automatic: from 4096 keys the split kernel
- * reads K in whole 256-byte rows through LDS-DMA, below straight into
- * registers; 1 = registers, 2 = LDS-DMA), "prefill_force_generic",
+ * Hkv allows), "decode_kdma" (0 = automatic: from 4096 keys, and for the
+ * one-workgroup-per-head plans, the split kernel reads K in whole 256-byte
+ * rows through LDS-DMA, otherwise straight into registers; 1 = registers,
+ * 2 = LDS-DMA), "prefill_force_generic",
  * "qkv_gemm_force_generic", "qkv_gemm_tokens_per_wave" (0 = automatic; 32, 64
  * or 128 tokens per wave of the 256 x 128-tile MFMA GEMM), "qkv_gemm_wide"
  * (0 = automatic, from 7168 tokens; 1 = never; 2 = whenever N is a multiple
@@ -376,7 +382,11 @@ int attn_prefill_plan(const void* q, const void* k, const void* v, const void* o
  * take the even and the odd key tiles and combine through LDS; 1 = never;
  * 2 = at any length), "decode_out_proj_fused" (see attn_decode_out_proj),
  * "graph_node_records" (0 = the updaters use node records; 1 = they read
- * every node back, as the reference does).
+ * every node back, as the reference does), "decode_whole_max_keys" (0 =
+ * automatic: contexts up to 384 keys are decoded by one workgroup per KV
+ * head whose fold writes the output, so attn_decode enqueues one kernel
+ * unless the merge node is asked for, and that merge kernel then exits at
+ * once; < 0 = never; > 0 = the longest such context).
  * Returns 0 or -1 for an unknown name. */
 int attn_set_option(const char* name, long value);
 

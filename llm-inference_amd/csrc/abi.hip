@@ -40,7 +40,8 @@ bool fits_u32(size_t v) { return v <= 0xffffffffull; }
 // What a merge node's kernel reads from its arguments, last written into each
 // (graph exec, merge node) pair by update_merge_attention_decode_node or
 // update_rope_and_store_kv_decode_nodes.  The merge kernels read only the
-// state count, the rotation switch and buffer pointers that never change
+// state count, the whole-context flag (which also sets the grid), the
+// rotation switch and buffer pointers that never change
 // (the fused RoPE form takes the position from the word the split kernel
 // leaves), so a patch that keeps count and switch is skipped -- but only when
 // they also equal the node's captured ones: an exec node holds either its
@@ -62,7 +63,9 @@ std::mutex g_merge_mu;
 std::unordered_map<MergePatchKey, uint64_t, MergePatchHash> g_merge_sig;
 constexpr size_t kMergeTableMax = 1u << 16;  // cleared when full (only costs patches)
 
-uint64_t merge_sig(const DecodeArgs& a) { return (uint64_t)a.nstate << 1 | (a.apply ? 1u : 0u); }
+uint64_t merge_sig(const DecodeArgs& a) {
+    return (uint64_t)a.nstate << 2 | (a.whole ? 2u : 0u) | (a.apply ? 1u : 0u);
+}
 
 // whether the exec node already runs the merge with `sig`, captured with
 // `captured`
@@ -279,6 +282,7 @@ int attn_set_option(const char* name, long value) {
     else if (!std::strcmp(name, "decode_heads_per_workgroup")) which = kOptDecodeHeadsPerGroup;
     else if (!std::strcmp(name, "decode_kdma")) which = kOptDecodeKdma;
     else if (!std::strcmp(name, "graph_node_records")) which = kOptGraphNodeRecords;
+    else if (!std::strcmp(name, "decode_whole_max_keys")) which = kOptDecodeWholeMaxKeys;
     else if (!std::strcmp(name, "qkv_gemm_force_generic")) which = kOptQkvGemmForceGeneric;
     else if (!std::strcmp(name, "qkv_gemm_tokens_per_wave")) which = kOptQkvGemmTokensPerWave;
     else if (!std::strcmp(name, "qkv_gemm_wide")) which = kOptQkvGemmWide;
@@ -597,7 +601,7 @@ int attn_decode_plan(size_t kv_len, size_t num_heads, size_t num_kv_heads, size_
     const size_t kvs = kv_stride ? kv_stride : num_kv_heads * head_dim;
     const DecodePlan p = plan_decode((uint32_t)kv_len, (uint32_t)num_heads,
                                      (uint32_t)num_kv_heads, (uint32_t)head_dim, kvs, q,
-                                     k_cache, v_cache, device);
+                                     k_cache, v_cache, device, true);
     out[0] = (uint32_t)p.path;
     out[1] = p.nsplit;
     out[2] = p.chunk;
@@ -607,9 +611,13 @@ int attn_decode_plan(size_t kv_len, size_t num_heads, size_t num_kv_heads, size_
 }
 
 // Enqueue an MFMA decode plan as the reference does: the split kernel
-// (*attention_node) then the merge kernel (*merge_node).
+// (*attention_node) then the merge kernel (*merge_node).  A whole-context
+// plan is the split kernel alone, unless the caller asks for the merge node
+// (a graph whose updaters may move to a longer context): then the merge
+// kernel is enqueued too and exits at once while the plan stays whole.
 static int enqueue_decode(DecodeArgs& a, int device, bool rope, hipStream_t stream,
                           hipGraphNode_t* attention_node, hipGraphNode_t* merge_node) {
+    a.whole_ok = 1;
     const DecodePlan p = replan_decode(a, device);
     if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
     hipError_t e = launch_decode_split(a, p, stream, rope);
@@ -619,6 +627,7 @@ static int enqueue_decode(DecodeArgs& a, int device, bool rope, hipStream_t stre
         e = captured_node(stream, attention_node);
         if (e != hipSuccess) return (int)e;
     }
+    if (p.whole && !merge_node) return 0;
     e = launch_decode_merge(a, stream, rope);
     if (e != hipSuccess) return (int)e;
     remember_launch<DecodeArgs>(stream);
@@ -648,7 +657,7 @@ int attn_decode(const attn_f16_t* q, const attn_f16_t* k_cache, const attn_f16_t
     if (e != hipSuccess) return (int)e;
     const DecodePlan p = plan_decode((uint32_t)kv_len, (uint32_t)num_heads,
                                      (uint32_t)num_kv_heads, (uint32_t)head_dim, kvs, q,
-                                     k_cache, v_cache, device);
+                                     k_cache, v_cache, device, true);
     if (p.path == 0) {
         // one kernel: both node handles name it (the merge patcher is a no-op)
         GenericAttnArgs g{};
@@ -732,7 +741,7 @@ int attn_rope_store_kv_decode(attn_f16_t* q, const attn_f16_t* k, const attn_f16
     if (e != hipSuccess) return (int)e;
     const DecodePlan p = plan_decode((uint32_t)kv_len, (uint32_t)num_heads,
                                      (uint32_t)num_kv_heads, (uint32_t)head_dim, kvs, q,
-                                     k_cache, v_cache, device);
+                                     k_cache, v_cache, device, true);
     if (p.path == 0 || !host_ok) {
         if (attention_node || merge_node) return (int)hipErrorInvalidValue;
         const int rc = attn_rope_store_kv(q, const_cast<attn_f16_t*>(k), v, k_cache, v_cache,
@@ -835,6 +844,8 @@ int attn_decode_out_proj(const attn_f16_t* q, const attn_f16_t* k_cache, const a
                         (size_t)o.row_blocks * sizeof(uint32_t);
     o.y_part = static_cast<float*>(out_proj_workspace);
     o.counters = reinterpret_cast<uint32_t*>(static_cast<char*>(out_proj_workspace) + part);
+    // whole_ok = 0: the fused form always splits, so that its merge node stays
+    // a merge at every context an updater moves it to
     const DecodePlan p = replan_decode(a, device);
     if (p.path < 1 || p.path > 3 || !out_proj_fused_ok(o)) return two_launches();
     e = launch_decode_split(a, p, stream, false);
@@ -877,6 +888,7 @@ static hipError_t replan_merge_node(hipGraphExec_t graph_exec, hipGraphNode_t no
     void* args[1] = {&a};
     params.kernelParams = args;
     params.extra = nullptr;
+    params.gridDim = decode_merge_grid(a);
     return hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
 }
 

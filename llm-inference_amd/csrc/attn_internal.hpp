@@ -103,6 +103,9 @@ struct DecodeArgs {
     uint32_t nsplit;     // context splits per KV head (patched)
     uint32_t chunk;      // keys per split (patched)
     uint32_t nstate;     // partial states per query head (patched)
+    uint32_t whole_ok;   // the caller's launch may run as one kernel (see plan_decode)
+    uint32_t whole;      // one split per KV-head group: the split kernel writes the
+                         // output (and q rotated), the merge kernel exits (patched)
     float scale_log2;    // log2(e) / sqrt(D)
     // fused RoPE + KV append of the decoded token (the ROPE kernel variants):
     // q rotated in registers by the split kernel and in place by the merge
@@ -183,11 +186,14 @@ struct DecodePlan {
     uint32_t block;    // threads per split workgroup
     uint32_t groups;   // KV-head groups (grid of the split workgroups: nsplit x groups)
     uint32_t kdma;     // 1: the split kernel reads K through LDS-DMA in whole rows
+    uint32_t whole;    // 1: one split per KV-head group and no merge work
 };
 
+// allow_whole: the launch may be one kernel for short contexts (callers that
+// do not need the merge kernel's separate node)
 DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_heads,
                        uint32_t head_dim, uint64_t kv_stride, const void* q, const void* k,
-                       const void* v, int device);
+                       const void* v, int device, bool allow_whole);
 // Recompute the split/chunk fields of an argument struct for its kv_len and
 // return the plan, whose path (heads per workgroup) also depends on kv_len.
 // Used by launch and by the graph-node updaters (same plan for the same L):
@@ -196,6 +202,7 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
 DecodePlan replan_decode(DecodeArgs& a, int device);
 int decode_hpw(int path);                        // KV heads per split workgroup (0: generic)
 dim3 decode_grid(const DecodeArgs& a, const DecodePlan& p);  // the split kernel's grid
+dim3 decode_merge_grid(const DecodeArgs& a);                  // the merge kernel's grid
 // Enqueues the split kernel (followed by launch_decode_merge).
 hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream,
                                bool rope = false);
@@ -288,7 +295,8 @@ enum Option {
     kOptPrefillKeyHalves = 11,    // 0 = automatic; 1 = never; 2 = 32-query tiles whose key tiles two 4-wave groups split
     kOptDecodeKdma = 12,          // 0 = automatic; 1 = K in registers; 2 = K through LDS-DMA
     kOptGraphNodeRecords = 13,    // 0 = updaters use the nodes recorded at capture; 1 = read nodes back
-    kOptCount = 14
+    kOptDecodeWholeMaxKeys = 14,  // 0 = automatic; < 0 never; > 0 longest one-kernel context
+    kOptCount = 15
 };
 long get_option(int which);
 

@@ -1,7 +1,8 @@
 // attn_decode_noalloc: Flash-Decode without a caller workspace, for callers
 // that cannot allocate device memory (code under graph capture that must not
 // call hipMalloc, tight serving loops, harnesses that forbid it).  It runs the
-// same plan and kernels as attn_decode (split kernel, merge kernel); the
+// same plan and kernels as attn_decode (split kernel, merge kernel; the split
+// kernel alone for the short contexts decoded by one workgroup per KV head); the
 // partial states (D fp16 outputs and two floats per query head and split) live in a
 // file-scope device array instead of the caller's partial_out/max/sum.
 //
@@ -77,7 +78,7 @@ extern "C" int attn_decode_noalloc(const attn_f16_t* q, const attn_f16_t* k_cach
     if (e != hipSuccess) return (int)e;
     const DecodePlan p = plan_decode((uint32_t)kv_len, (uint32_t)num_heads,
                                      (uint32_t)num_kv_heads, (uint32_t)head_dim, kvs, q,
-                                     k_cache, v_cache, device);
+                                     k_cache, v_cache, device, true);
     if (p.path == 0) {
         // shapes off the MFMA path take attn_decode's generic kernel, which
         // has no partial states
@@ -106,9 +107,10 @@ extern "C" int attn_decode_noalloc(const attn_f16_t* q, const attn_f16_t* k_cach
     a.group = (uint32_t)(num_heads / num_kv_heads);
     a.head_dim = (uint32_t)head_dim;
     a.scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)head_dim));
+    a.whole_ok = 1;  // as attn_decode without node handles
     const DecodePlan pr = replan_decode(a, device);
     if (pr.path < 1 || pr.path > 3 || pr.nstate != p.nstate) return (int)hipErrorInvalidValue;
     e = launch_decode_split(a, pr, stream, false);
-    if (e != hipSuccess) return (int)e;
+    if (e != hipSuccess || pr.whole) return (int)e;
     return (int)launch_decode_merge(a, stream, false);
 }

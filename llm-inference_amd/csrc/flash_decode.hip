@@ -62,6 +62,10 @@ constexpr int kMaxSplits = 1024;
 constexpr uint32_t kOneHeadMaxKeys = 12288;
 // shortest context whose split kernel reads K through LDS-DMA (see plan_decode)
 constexpr uint32_t kDmaMinKeys = 4096;
+// shortest chunk of a split workgroup with two KV heads (see plan_decode)
+constexpr uint32_t kTwoHeadMinChunk = 160;
+// longest context decoded by one workgroup per KV head (see plan_decode)
+constexpr uint32_t kWholeMaxKeys = 384;
 constexpr int kAccPitch = kD + 4;
 // cache-policy bit nt (non-temporal) of raw buffer loads
 constexpr int kNT = 2;
@@ -267,6 +271,14 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     float l_run = 0.f;
     constexpr uint32_t kStep = 32u * kPhases;
     uint32_t b = 32u * phase;
+    // whole-context plans with RoPE: this workgroup is the only reader of its
+    // query heads, so it writes them back rotated once every wave has read
+    // them (the phase-0 wave of each head keeps its rotated copy)
+    f16x8 qkeep[4];
+    if constexpr (ROPE) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) qkeep[s] = f16x8{};
+    }
     // wave-uniform: a wave whose first batch lies past the chunk (short
     // contexts) has no keys and goes straight to the fold
     if (b < nk) {
@@ -295,10 +307,13 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
             for (int s = 0; s < 4; ++s) qb[s] = f16x8{};
         }
 
-        // the first two batches of this wave
+        // the first two batches of this wave (wave-uniform `two`: a wave with
+        // one batch issues no loads past the chunk, whose address processing
+        // would still take the CU's load pipeline)
         KVBatch<KDMA> A, B;
+        const bool two = b + kStep < nk;
         load(b, A, 0);
-        load(b + kStep, B, 1);
+        if (two) load(b + kStep, B, 1);
         TL(if (tid == 0) tl[1] = tl_now();)
 
         if constexpr (ROPE) {
@@ -308,6 +323,10 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
 #pragma unroll
                 for (int s = 0; s < 2; ++s)
                     rope_rotate8(qb[s], qb[s + 2], rc[s], rs[s], qb[s], qb[s + 2]);
+            }
+            if (a.whole) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) qkeep[s] = qb[s];
             }
         }
 
@@ -395,31 +414,56 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
         // into the loop test has exactly batches A and B in flight (the last
         // pair is peeled off below), so the compiler's waits stay vmcnt(16) for
         // A and let B's loads overlap A's compute.
-        while (b + 2 * kStep < nk) {
+        if (!two) {
+            // one batch, nothing issued after it
+            __builtin_amdgcn_sched_barrier(0);
+            compute(A, 0, b, false);
+        } else {
+            while (b + 2 * kStep < nk) {
+                __builtin_amdgcn_sched_barrier(0);
+                compute(A, 0, b, true);
+                load(b + 2 * kStep, A, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(B, 1, b + kStep, true);
+                load(b + 3 * kStep, B, 1);
+                b += 2 * kStep;
+            }
             __builtin_amdgcn_sched_barrier(0);
             compute(A, 0, b, true);
-            load(b + 2 * kStep, A, 0);
             __builtin_amdgcn_sched_barrier(0);
-            compute(B, 1, b + kStep, true);
-            load(b + 3 * kStep, B, 1);
-            b += 2 * kStep;
+            // keys past the chunk are masked (p = 0)
+            if (b + kStep < nk) compute(B, 1, b + kStep, false);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        compute(A, 0, b, true);
-        __builtin_amdgcn_sched_barrier(0);
-        // keys past the chunk are masked (p = 0)
-        if (b + kStep < nk) compute(B, 1, b + kStep, false);
         TL(if (lane == 0) tl[2 + wave] = tl_now();)
     }
 
     // per-query sum over the four lane groups (the max is already shared)
     l_run += xor_lane(l_run, 16);
     l_run += xor_lane(l_run, 32);
+    // lanes (gq, n < G) of the phase-0 wave of KV head g: query head g G + n,
+    // dims 32s + 8gq .. + 7 of q, rotated (whole-context RoPE plans)
+    auto store_q_rotated = [&]() {
+        if constexpr (ROPE) {
+            if (a.whole && a.apply && phase == 0 && (uint32_t)n < G) {
+                f16* const qh = a.q_rot + (uint64_t)(g * G + n) * kD + 8u * gq;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) st16(qh + 32 * s, qkeep[s]);
+            }
+        }
+    };
     if (solo) {
         // the split's state is this wave's (what the fold below would give:
         // the other waves of the head carry weight 0); lane (gq, n < G) holds
         // dims 32gq + 8i + mt = acc[mt][i] of query n
-        if ((uint32_t)n < G) {
+        if ((uint32_t)n < G && a.whole) {
+            // the only split: its state is the output
+            const float inv = 1.0f / l_run;
+            f16* const oh = a.out + (uint64_t)(g * G + n) * kD + 32u * gq;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int mt = 0; mt < 8; ++mt) oh[8 * i + mt] = (f16)(acc[mt][i] * inv);
+        } else if ((uint32_t)n < G) {
             const BufRsrc rpo = make_rsrc(a.part_out, a.num_heads * a.nstate * kD * 2u);
             const uint32_t st = (g * G + (uint32_t)n) * a.nstate + c;
             const float inv = 1.0f / l_run;  // l_run >= 1: the chunk's maximum has weight 1
@@ -437,6 +481,7 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
                 a.part_sum[st] = l_run;
             }
         }
+        store_q_rotated();  // the other waves returned before reading q
         TL(if (lane == 0) {
                tl[14] = tl[10] = tl_now();
                wait_stores();
@@ -493,10 +538,18 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
             num += wt * aw[ph];
             den += wt * lw[ph];
         }
-        const uint32_t st = row * a.nstate + c;  // state index within the head group
         // the state's output normalised by its own sum (den >= 1: the chunk's
         // maximum has weight 1), in fp16
         const float inv = 1.0f / den;
+        if (a.whole) {
+            // the only split: the state is the output of query head
+            // (grp HPW + hl) G + qn
+            f16* const o = a.out + (uint64_t)((grp * HPW + hl) * G + qn) * kD + d;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = (f16)(num[e] * inv);
+            continue;
+        }
+        const uint32_t st = row * a.nstate + c;  // state index within the head group
         const f16x4 o = {(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv),
                          (f16)(num[3] * inv)};
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o), rpo,
@@ -507,6 +560,7 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
             a.part_sum[sg] = den;
         }
     }
+    store_q_rotated();  // every wave of this workgroup has read q (barrier above)
     TL(if (tid == 0) {
            tl[10] = tl_now();
            wait_stores();
@@ -525,6 +579,7 @@ constexpr int kMergeRound = 4;   // splits per lane per round of loads
 // (wave_max, wave_sum).
 template <bool ROPE>
 __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
+    if (a.whole) return;  // the split kernel wrote the output (and q)
     const uint32_t lane = threadIdx.x;
     const uint32_t h = blockIdx.x;
     const uint32_t d0 = blockIdx.y * kMergeDims;
@@ -636,7 +691,7 @@ int decode_path_of_symbol(const void* fn, bool rope) {
 
 DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_heads,
                        uint32_t head_dim, uint64_t kv_stride, const void* q, const void* k,
-                       const void* v, int device) {
+                       const void* v, int device, bool allow_whole) {
     DecodePlan p{0, 1, kv_len, 1, 256, 1, 0};
     const uint32_t G = num_heads / num_kv_heads;
     const bool mfma_ok = head_dim == kD && G >= 1 && G <= 16 && kv_stride % 8 == 0 &&
@@ -665,8 +720,13 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
     const uint32_t units = (kv_len + unit - 1) / unit;
     const uint32_t cus = (uint32_t)std::max(1, device_cu_count(device));
     const long sopt = get_option(kOptDecodeSplits);
-    // one 8-wave workgroup per CU
-    const uint32_t target = sopt > 0 ? (uint32_t)sopt : std::max(1u, (cus + groups - 1) / groups);
+    // one 8-wave workgroup per CU; with two KV heads per workgroup, chunks of
+    // at least kTwoHeadMinChunk keys even if CUs stay idle (L = 16384: 103
+    // splits of 160 keys 10.30 us, 128 of 128 keys 10.79 us; 14336: 9.86
+    // against 10.19 us; equal or better from 13312 to 19456 keys)
+    uint32_t target = sopt > 0 ? (uint32_t)sopt : std::max(1u, (cus + groups - 1) / groups);
+    if (sopt <= 0 && hpw == 2)
+        target = std::min(target, std::max(1u, (kv_len + kTwoHeadMinChunk - 1) / kTwoHeadMinChunk));
     uint32_t nsplit = std::max(1u, std::min<uint32_t>({target, units, (uint32_t)kMaxSplits}));
     // at least 16 keys per split: with chunks of >= KV_CHUNK (12) keys the
     // states fit the caller's Hq * ceil(L / 12)-state workspace
@@ -675,6 +735,21 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
     const uint64_t max_rows = (0xffffffffull - kD * 2) / (kv_stride * 2);
     while (chunk > max_rows && chunk > 16u) chunk -= unit;
     nsplit = (kv_len + chunk - 1) / chunk;
+    // short contexts, when the caller allows one kernel: one workgroup per
+    // KV-head group takes the whole context and its fold writes the output
+    // (the merge's kernel boundary and partial-state round trip, ~2.3 us of a
+    // 254-key call, are gone).  Its K goes through LDS-DMA in whole rows: the
+    // four workgroups are bound by their CUs' load pipelines, which the
+    // A-layout reads (16 rows x 64 B per instruction) use half as well
+    // (L = 254: 3.81 us against 4.92 us with K in registers and 4.67 us split;
+    // 384 keys: 4.48 against 4.67 split)
+    const long wopt = get_option(kOptDecodeWholeMaxKeys);
+    const uint64_t whole_max = wopt < 0 ? 0u : wopt > 0 ? (uint64_t)wopt : kWholeMaxKeys;
+    if (allow_whole && sopt <= 0 && kv_len <= whole_max && kv_len <= max_rows) {
+        nsplit = 1;
+        chunk = (kv_len + unit - 1) / unit * unit;
+        p.whole = 1;
+    }
     p.nsplit = nsplit;
     p.chunk = chunk;
     p.nstate = nsplit;  // one folded state per split and query head
@@ -682,16 +757,17 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
     // kDmaMinKeys keys); below, the call is latency-bound and K goes straight
     // into registers in the MFMA layout, one step shorter per batch
     const long kopt = get_option(kOptDecodeKdma);
-    p.kdma = kopt == 1 ? 0u : kopt == 2 ? 1u : (kv_len >= kDmaMinKeys ? 1u : 0u);
+    p.kdma = kopt == 1 ? 0u : kopt == 2 ? 1u : (kv_len >= kDmaMinKeys || p.whole ? 1u : 0u);
     return p;
 }
 
 DecodePlan replan_decode(DecodeArgs& a, int device) {
     const DecodePlan p = plan_decode(a.kv_len, a.num_heads, a.num_kv_heads, a.head_dim,
-                                     a.kv_stride, a.q, a.k, a.v, device);
+                                     a.kv_stride, a.q, a.k, a.v, device, a.whole_ok != 0);
     a.nsplit = p.nsplit;
     a.chunk = p.chunk;
     a.nstate = p.nstate;
+    a.whole = p.whole;
     return p;
 }
 
@@ -700,6 +776,12 @@ DecodePlan replan_decode(DecodeArgs& a, int device) {
 dim3 decode_grid(const DecodeArgs& a, const DecodePlan& p) {
     const uint32_t phases = 8u / (uint32_t)decode_hpw(p.path);
     return a.chunk <= 64u * phases ? dim3(p.groups, a.nsplit) : dim3(a.nsplit, p.groups);
+}
+
+// one workgroup per query head and 4 output dims; one workgroup, which
+// exits at once, for a whole-context plan
+dim3 decode_merge_grid(const DecodeArgs& a) {
+    return a.whole ? dim3(1, 1) : dim3(a.num_heads, kD / kMergeDims);
 }
 
 #if defined(ATTN_DECODE_TIMELINE)
@@ -745,8 +827,8 @@ hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream, bool rop
 #else
     void* args[1] = {const_cast<DecodeArgs*>(&a)};
 #endif
-    return hipLaunchKernel(decode_merge_symbol(rope), dim3(a.num_heads, kD / kMergeDims),
-                           dim3(64), args, 0, stream);
+    return hipLaunchKernel(decode_merge_symbol(rope), decode_merge_grid(a), dim3(64), args, 0,
+                           stream);
 }
 
 }  // namespace attn

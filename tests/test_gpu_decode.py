@@ -197,6 +197,35 @@ def test_decode_other_group_sizes(attn, gpu, Hq, Hkv):
     assert_close(got, expected(q, k, v, L, Hq, Hkv, D), 2e-3, 1e-2, f"{Hq}/{Hkv}")
 
 
+@pytest.mark.parametrize("L", [1, 20, 32, 33, 100, 254, 255, 383, 384, 385])
+def test_decode_whole_context_plans(attn, gpu, L):
+    """Up to 384 keys one workgroup per KV head takes the whole context (K
+    through LDS-DMA, or straight into registers with decode_kdma = 1) and its
+    fold writes the output (one kernel): within tolerance of the oracle, as
+    is the two-kernel plan of the same inputs (option decode_whole_max_keys
+    = -1), and the plan reports one split."""
+    q, k, v = smol_inputs(L, seed=300 + L)
+    plan = attn.decode_plan(L, 16, 4, 128)
+    assert (plan["nsplit"] == 1 and plan["nstate"] == 1) == (L <= 384), plan
+    print(f"[case] decode whole-context L={L} plan={plan}", flush=True)
+    e = expected(q, k, v, L)
+    got = run_decode(attn, gpu, q, k, v, L, 16, 4, 128)
+    assert_close(got, e, 2e-3, 1e-2, f"whole L={L}")
+    attn.set_option("decode_kdma", 1)
+    try:
+        reg = run_decode(attn, gpu, q, k, v, L, 16, 4, 128)
+    finally:
+        attn.set_option("decode_kdma", 0)
+    assert np.array_equal(reg, got), "K paths differ"
+    attn.set_option("decode_whole_max_keys", -1)
+    try:
+        assert attn.decode_plan(L, 16, 4, 128)["nsplit"] > 1 or L <= 16
+        two = run_decode(attn, gpu, q, k, v, L, 16, 4, 128)
+    finally:
+        attn.set_option("decode_whole_max_keys", 0)
+    assert_close(two, e, 2e-3, 1e-2, f"two kernels L={L}")
+
+
 def test_decode_closed_forms(attn, gpu):
     # one key: the output is V[0] bit for bit; identical keys: the mean of V
     q, k, v = smol_inputs(1, seed=11)

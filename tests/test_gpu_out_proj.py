@@ -157,9 +157,15 @@ def test_decode_out_proj_smollm3(attn, gpu, fused, L, beta):
     y, attn_out = c.fused(beta)
     assert c.counters_zero()
     check_step(c, beta, y, attn_out)
-    # the pair of launches it replaces: the same attention within fp32
-    # merge-order rounding, the same projection within the north-star tolerance
-    y2, attn2 = c.two_launches(beta)
+    # the pair of launches it replaces, with the same split plan (short
+    # contexts would otherwise be decoded in one kernel, without fp16 partial
+    # states): the same attention within fp32 merge-order rounding, the same
+    # projection within the north-star tolerance
+    attn.set_option("decode_whole_max_keys", -1)
+    try:
+        y2, attn2 = c.two_launches(beta)
+    finally:
+        attn.set_option("decode_whole_max_keys", 0)
     assert ulp_diff(attn_out, attn2).max() <= 1
     assert_close(y, y2, 2e-3, 1e-2, "fused vs two launches")
 
