@@ -359,10 +359,10 @@ int attn_prefill_plan(const void* q, const void* k, const void* v, const void* o
  * "decode_force_generic", "decode_splits" (0 = automatic),
  * "decode_heads_per_workgroup" (0 = automatic: 1 up to 12288 keys, 2 above
  * when Hkv is even; 1, 2 or 4 KV heads per split workgroup, reduced to what
- * Hkv allows), "decode_kdma" (0 = automatic: from 4096 keys, and for the
- * one-workgroup-per-head plans, the split kernel reads K in whole 256-byte
- * rows through LDS-DMA, otherwise straight into registers; 1 = registers,
- * 2 = LDS-DMA), "prefill_force_generic",
+ * Hkv allows), "decode_kdma" (0 = automatic: from 4096 keys with more than
+ * 64 keys per split, and for the one-workgroup-per-head plans, the split
+ * kernel reads K in whole 256-byte rows through LDS-DMA, otherwise straight
+ * into registers; 1 = registers, 2 = LDS-DMA), "prefill_force_generic",
  * "qkv_gemm_force_generic", "qkv_gemm_tokens_per_wave" (0 = automatic; 32, 64
  * or 128 tokens per wave of the 256 x 128-tile MFMA GEMM), "qkv_gemm_wide"
  * (0 = automatic, from 7168 tokens; 1 = never; 2 = whenever N is a multiple

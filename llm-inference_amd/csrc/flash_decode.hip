@@ -64,6 +64,8 @@ constexpr uint32_t kOneHeadMaxKeys = 12288;
 constexpr uint32_t kDmaMinKeys = 4096;
 // shortest chunk of a split workgroup with two KV heads (see plan_decode)
 constexpr uint32_t kTwoHeadMinChunk = 160;
+// longest chunk whose batches one wave per head takes (flash_decode_split)
+constexpr uint32_t kSoloMaxKeys = 64;
 // longest context decoded by one workgroup per KV head (see plan_decode)
 constexpr uint32_t kWholeMaxKeys = 384;
 constexpr int kAccPitch = kD + 4;
@@ -255,10 +257,11 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
             __syncthreads();
         }
     }
-    // a chunk of at most one 32-key batch (short contexts): only the phase-0
-    // waves have keys; they store their states straight from registers and
-    // the others have nothing to do
-    const bool solo = a.chunk <= 32u;
+    // a chunk of at most kSoloMaxKeys keys (short contexts): the phase-0
+    // wave of each head takes every batch of the chunk (both in flight) and
+    // stores the state straight from registers; the other waves have nothing
+    // to do (no LDS fold, no barrier)
+    const bool solo = a.chunk <= kSoloMaxKeys;
     if (solo && phase != 0) return;
 
     f32x4 acc[8];
@@ -269,7 +272,8 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     // rescale factor 1 without special cases
     float m_run = -1.0e30f;
     float l_run = 0.f;
-    constexpr uint32_t kStep = 32u * kPhases;
+    // batches b, b + step, ... of the chunk are this wave's
+    const uint32_t kStep = solo ? 32u : 32u * kPhases;
     uint32_t b = 32u * phase;
     // whole-context plans with RoPE: this workgroup is the only reader of its
     // query heads, so it writes them back rotated once every wave has read
@@ -756,8 +760,12 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
     // K through LDS-DMA in whole 256-byte rows once the call streams (from
     // kDmaMinKeys keys); below, the call is latency-bound and K goes straight
     // into registers in the MFMA layout, one step shorter per batch
+    // (chunks of at most kSoloMaxKeys, which one wave per head takes, keep K
+    // in registers: L = 4096, 64-key chunks: 6.35 against 6.60 us)
     const long kopt = get_option(kOptDecodeKdma);
-    p.kdma = kopt == 1 ? 0u : kopt == 2 ? 1u : (kv_len >= kDmaMinKeys || p.whole ? 1u : 0u);
+    p.kdma = kopt == 1   ? 0u
+             : kopt == 2 ? 1u
+                         : ((kv_len >= kDmaMinKeys && chunk > kSoloMaxKeys) || p.whole ? 1u : 0u);
     return p;
 }
 
