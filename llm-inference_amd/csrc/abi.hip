@@ -880,14 +880,17 @@ static hipError_t replan_split_node(hipGraphExec_t graph_exec, hipGraphNode_t no
     return hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
 }
 
-// Re-point a captured merge node at kv_len (its split count).
+// Re-point a captured merge node at kv_len (its split count; for a
+// whole-context plan the idle kernel).
 static hipError_t replan_merge_node(hipGraphExec_t graph_exec, hipGraphNode_t node,
-                                    hipKernelNodeParams& params, DecodeArgs& a, int device) {
+                                    hipKernelNodeParams& params, DecodeArgs& a, bool rope,
+                                    int device) {
     const DecodePlan p = replan_decode(a, device);
     if (p.path < 1 || p.path > 3) return hipErrorInvalidValue;
     void* args[1] = {&a};
     params.kernelParams = args;
     params.extra = nullptr;
+    params.func = const_cast<void*>(decode_merge_symbol(rope, a.whole != 0));
     params.gridDim = decode_merge_grid(a);
     return hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
 }
@@ -905,7 +908,8 @@ int attn_update_rope_decode_nodes(hipGraphExec_t graph_exec, hipGraphNode_t atte
         e = node_device(view, &device);
         if (e != hipSuccess) return (int)e;
         hipKernelNodeParams& params = view.params;
-        const bool ok = m ? params.func == decode_merge_symbol(true)
+        const bool ok = m ? (params.func == decode_merge_symbol(true, false) ||
+                             params.func == decode_merge_symbol(true, true))
                           : decode_path_of_symbol(params.func, true) != 0;
         if (!ok) return (int)hipErrorInvalidValue;
         DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(view.arg);
@@ -922,7 +926,7 @@ int attn_update_rope_decode_nodes(hipGraphExec_t graph_exec, hipGraphNode_t atte
         const DecodePlan p = replan_decode(a, device);
         if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
         if (merge_current(graph_exec, node, captured, merge_sig(a))) continue;
-        e = replan_merge_node(graph_exec, node, params, a, device);
+        e = replan_merge_node(graph_exec, node, params, a, true, device);
         if (e != hipSuccess) return (int)e;
         merge_patched(graph_exec, node, merge_sig(a));
     }
@@ -962,7 +966,8 @@ static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, siz
         return (int)hipGraphExecKernelNodeSetParams(graph_exec, node, &params);
     }
     const bool is_split = decode_path_of_symbol(params.func, false) != 0;
-    const bool is_merge = params.func == decode_merge_symbol();
+    const bool is_merge = params.func == decode_merge_symbol(false, false) ||
+                          params.func == decode_merge_symbol(false, true);
     if ((merge && !is_merge) || (!merge && !is_split)) return (int)hipErrorInvalidValue;
     DecodeArgs a = *reinterpret_cast<const DecodeArgs*>(view.arg);
     e = node_device(view, &device);
@@ -974,7 +979,7 @@ static int patch_decode_node(hipGraphExec_t graph_exec, hipGraphNode_t node, siz
     if (p.path < 1 || p.path > 3) return (int)hipErrorInvalidValue;
     // the exec node already reads this many states
     if (merge_current(graph_exec, node, captured, merge_sig(a))) return 0;
-    e = replan_merge_node(graph_exec, node, params, a, device);
+    e = replan_merge_node(graph_exec, node, params, a, false, device);
     if (e != hipSuccess) return (int)e;
     merge_patched(graph_exec, node, merge_sig(a));
     return 0;

@@ -208,7 +208,8 @@ hipError_t launch_decode_split(const DecodeArgs& a, const DecodePlan& p, hipStre
                                bool rope = false);
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream, bool rope = false);
 const void* decode_split_symbol(const DecodePlan& p, bool rope = false);
-const void* decode_merge_symbol(bool rope = false);
+// the merge kernel, or for a whole-context plan the kernel that does nothing
+const void* decode_merge_symbol(bool rope = false, bool whole = false);
 int decode_path_of_symbol(const void* fn, bool rope);  // 0 when not a split kernel
 
 // Decode attention's partial-state merge fused into the attention output

@@ -134,8 +134,9 @@ __device__ __forceinline__ uint64_t tl_xcc_id() { return (uint32_t)__builtin_amd
 // each XCD then taking both halves of the same cache rows), level at 254,
 // 4096 and 16384 keys.  Longer chunks keep (nsplit, Hkv / HPW): level from
 // 40960 to 98304 keys, but 26.3-27.9 against 25.9-26.3 us at 65536.
-template <int HPW, bool ROPE, bool KDMA>
+template <int HPW, bool ROPE, bool KDMA, bool WHOLE>
 __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
+    static_assert(!WHOLE || HPW == 1, "whole-context plans take one KV head per workgroup");
     constexpr int WAVES = 8;
     constexpr int kThreads = WAVES * 64;
     constexpr int kPhases = WAVES / HPW;  // waves sharing one KV head
@@ -161,9 +162,12 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     const int phase = wave / HPW;
     const int n = lane & 15;   // MFMA column (query head in group) / A row
     const int gq = lane >> 4;  // MFMA k-group / output row group
-    // a grid wider than the KV heads (a graph node re-planned for another
-    // heads-per-workgroup count) has nothing for its extra workgroups
-    if (grp * HPW >= a.num_kv_heads) return;
+    // The grid is exactly (Hkv / HPW) x nsplit: every launch and every graph
+    // node re-plan takes it from decode_grid.  No early exit tests the
+    // arguments: a branch on one costs the kernel a kernel-argument round
+    // trip before its other argument loads (~0.1 us per call at L = 32768,
+    // ~0.05 at 16384 together with the merge kernel's own, see
+    // flash_decode_merge_idle).
     TL(const uint64_t tl_t0 = tl_now();
        uint64_t* const tl = a.tl + (uint64_t)(blockIdx.y * gridDim.x + blockIdx.x) * kTlSplitWords;
        if (tid == 0) {
@@ -275,14 +279,6 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     // batches b, b + step, ... of the chunk are this wave's
     const uint32_t kStep = solo ? 32u : 32u * kPhases;
     uint32_t b = 32u * phase;
-    // whole-context plans with RoPE: this workgroup is the only reader of its
-    // query heads, so it writes them back rotated once every wave has read
-    // them (the phase-0 wave of each head keeps its rotated copy)
-    f16x8 qkeep[4];
-    if constexpr (ROPE) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) qkeep[s] = f16x8{};
-    }
     // wave-uniform: a wave whose first batch lies past the chunk (short
     // contexts) has no keys and goes straight to the fold
     if (b < nk) {
@@ -327,10 +323,6 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
 #pragma unroll
                 for (int s = 0; s < 2; ++s)
                     rope_rotate8(qb[s], qb[s + 2], rc[s], rs[s], qb[s], qb[s + 2]);
-            }
-            if (a.whole) {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) qkeep[s] = qb[s];
             }
         }
 
@@ -444,22 +436,22 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     // per-query sum over the four lane groups (the max is already shared)
     l_run += xor_lane(l_run, 16);
     l_run += xor_lane(l_run, 32);
-    // lanes (gq, n < G) of the phase-0 wave of KV head g: query head g G + n,
-    // dims 32s + 8gq .. + 7 of q, rotated (whole-context RoPE plans)
+    // whole-context plans with RoPE: this workgroup is the only reader of
+    // its query heads, so once every wave has read them it writes them back
+    // rotated, as the merge kernel does otherwise (lanes 0..7 of the phase-0
+    // wave of KV head g, query heads g G .. g G + G - 1)
     auto store_q_rotated = [&]() {
         if constexpr (ROPE) {
-            if (a.whole && a.apply && phase == 0 && (uint32_t)n < G) {
-                f16* const qh = a.q_rot + (uint64_t)(g * G + n) * kD + 8u * gq;
-#pragma unroll
-                for (int s = 0; s < 4; ++s) st16(qh + 32 * s, qkeep[s]);
-            }
+            if (WHOLE && a.apply && phase == 0 && lane < 8)
+                for (uint32_t qn = 0; qn < G; ++qn)
+                    rotate_q_head(a, g * G + qn, (uint32_t)lane, a.row);
         }
     };
     if (solo) {
         // the split's state is this wave's (what the fold below would give:
         // the other waves of the head carry weight 0); lane (gq, n < G) holds
         // dims 32gq + 8i + mt = acc[mt][i] of query n
-        if ((uint32_t)n < G && a.whole) {
+        if (WHOLE && (uint32_t)n < G) {
             // the only split: its state is the output
             const float inv = 1.0f / l_run;
             f16* const oh = a.out + (uint64_t)(g * G + n) * kD + 32u * gq;
@@ -545,7 +537,7 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
         // the state's output normalised by its own sum (den >= 1: the chunk's
         // maximum has weight 1), in fp16
         const float inv = 1.0f / den;
-        if (a.whole) {
+        if constexpr (WHOLE) {
             // the only split: the state is the output of query head
             // (grp HPW + hl) G + qn
             f16* const o = a.out + (uint64_t)((grp * HPW + hl) * G + qn) * kD + d;
@@ -583,7 +575,6 @@ constexpr int kMergeRound = 4;   // splits per lane per round of loads
 // (wave_max, wave_sum).
 template <bool ROPE>
 __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
-    if (a.whole) return;  // the split kernel wrote the output (and q)
     const uint32_t lane = threadIdx.x;
     const uint32_t h = blockIdx.x;
     const uint32_t d0 = blockIdx.y * kMergeDims;
@@ -656,6 +647,13 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
     }
 }
 
+// The merge node of a whole-context plan (the split kernel wrote the output
+// and q): nothing to do.  A kernel of its own, so that the merge kernel
+// proper tests no flag before its loads (a branch on an argument costs it a
+// kernel-argument round trip of its own, ~0.3 us per call at L = 32768).
+template <bool ROPE>
+__global__ __launch_bounds__(64) void flash_decode_merge_idle(DecodeArgs) {}
+
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -663,25 +661,35 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 int decode_hpw(int path) { return path == 1 ? 4 : path == 2 ? 2 : path == 3 ? 1 : 0; }
 
 template <bool ROPE, bool KDMA>
-const void* split_symbol_of(int path) {
-    if (path == 1) return reinterpret_cast<const void*>(&flash_decode_split<4, ROPE, KDMA>);
-    if (path == 2) return reinterpret_cast<const void*>(&flash_decode_split<2, ROPE, KDMA>);
-    if (path == 3) return reinterpret_cast<const void*>(&flash_decode_split<1, ROPE, KDMA>);
+const void* split_symbol_of(int path, bool whole) {
+    if (whole) return path == 3 ? reinterpret_cast<const void*>(
+                                      &flash_decode_split<1, ROPE, KDMA, true>)
+                                : nullptr;
+    if (path == 1) return reinterpret_cast<const void*>(&flash_decode_split<4, ROPE, KDMA, false>);
+    if (path == 2) return reinterpret_cast<const void*>(&flash_decode_split<2, ROPE, KDMA, false>);
+    if (path == 3) return reinterpret_cast<const void*>(&flash_decode_split<1, ROPE, KDMA, false>);
     return nullptr;
 }
 
-// path 1/2/3: 4/2/1 KV heads per workgroup; kdma: K through LDS-DMA
-const void* split_symbol(int path, bool rope, bool kdma) {
-    if (rope) return kdma ? split_symbol_of<true, true>(path) : split_symbol_of<true, false>(path);
+// path 1/2/3: 4/2/1 KV heads per workgroup; kdma: K through LDS-DMA; whole:
+// the one-split plan whose fold writes the output (path 3 only)
+const void* split_symbol(int path, bool rope, bool kdma, bool whole) {
+    if (rope)
+        return kdma ? split_symbol_of<true, true>(path, whole)
+                    : split_symbol_of<true, false>(path, whole);
     if (path < 1 || path > 3) return generic_attention_symbol();
-    return kdma ? split_symbol_of<false, true>(path) : split_symbol_of<false, false>(path);
+    return kdma ? split_symbol_of<false, true>(path, whole)
+                : split_symbol_of<false, false>(path, whole);
 }
 
 const void* decode_split_symbol(const DecodePlan& p, bool rope) {
-    return split_symbol(p.path, rope, p.kdma != 0);
+    return split_symbol(p.path, rope, p.kdma != 0, p.whole != 0);
 }
 
-const void* decode_merge_symbol(bool rope) {
+const void* decode_merge_symbol(bool rope, bool whole) {
+    if (whole)
+        return rope ? reinterpret_cast<const void*>(&flash_decode_merge_idle<true>)
+                    : reinterpret_cast<const void*>(&flash_decode_merge_idle<false>);
     return rope ? reinterpret_cast<const void*>(&flash_decode_merge<true>)
                 : reinterpret_cast<const void*>(&flash_decode_merge<false>);
 }
@@ -689,7 +697,8 @@ const void* decode_merge_symbol(bool rope) {
 int decode_path_of_symbol(const void* fn, bool rope) {
     for (int path = 1; path <= 3; ++path)
         for (int kdma = 0; kdma < 2; ++kdma)
-            if (fn == split_symbol(path, rope, kdma != 0)) return path;
+            for (int whole = 0; whole < 2; ++whole)
+                if (fn && fn == split_symbol(path, rope, kdma != 0, whole != 0)) return path;
     return 0;
 }
 
@@ -749,7 +758,7 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
     // 384 keys: 4.48 against 4.67 split)
     const long wopt = get_option(kOptDecodeWholeMaxKeys);
     const uint64_t whole_max = wopt < 0 ? 0u : wopt > 0 ? (uint64_t)wopt : kWholeMaxKeys;
-    if (allow_whole && sopt <= 0 && kv_len <= whole_max && kv_len <= max_rows) {
+    if (allow_whole && sopt <= 0 && hpw == 1 && kv_len <= whole_max && kv_len <= max_rows) {
         nsplit = 1;
         chunk = (kv_len + unit - 1) / unit * unit;
         p.whole = 1;
@@ -835,8 +844,8 @@ hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream, bool rop
 #else
     void* args[1] = {const_cast<DecodeArgs*>(&a)};
 #endif
-    return hipLaunchKernel(decode_merge_symbol(rope), decode_merge_grid(a), dim3(64), args, 0,
-                           stream);
+    return hipLaunchKernel(decode_merge_symbol(rope, a.whole != 0), decode_merge_grid(a),
+                           dim3(64), args, 0, stream);
 }
 
 }  // namespace attn
