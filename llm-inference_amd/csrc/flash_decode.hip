@@ -155,6 +155,15 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
         return reinterpret_cast<float*>(&s_w[w][0]) + q * kAccPitch;
     };
 
+    // every argument fetched at entry, in one batch: left to the compiler,
+    // some were fetched just before the first K/V loads (the score scale,
+    // used on both batch paths, the V pointer), whose issue then waited for
+    // them (C3 +0.1 us per call)
+    asm volatile("" ::"s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kv_stride), "s"(a.kv_len),
+                 "s"(a.group), "s"(a.chunk), "s"(a.nstate), "s"(a.scale_log2));
+    if constexpr (ROPE)
+        asm volatile("" ::"s"(a.q_rot), "s"(a.k_dst), "s"(a.v_dst), "s"(a.k_src), "s"(a.v_src),
+                     "s"(a.cos_t), "s"(a.sin_t), "s"(a.row), "s"(a.apply));
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -307,24 +316,20 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
             for (int s = 0; s < 4; ++s) qb[s] = f16x8{};
         }
 
-        // the first two batches of this wave (wave-uniform `two`: a wave with
-        // one batch issues no loads past the chunk, whose address processing
-        // would still take the CU's load pipeline)
         KVBatch<KDMA> A, B;
-        const bool two = b + kStep < nk;
-        load(b, A, 0);
-        if (two) load(b + kStep, B, 1);
-        TL(if (tid == 0) tl[1] = tl_now();)
-
-        if constexpr (ROPE) {
-            // dims 32s + 8gq + i (s = 0, 1) pair with 64 more (s + 2): the lane
-            // holds both halves of 16 rotation pairs (rope.hip.cpp:44-58)
-            if (qlane && a.apply) {
+        // after the first loads are issued: q rotated in registers
+        auto rotate_q = [&]() {
+            TL(if (tid == 0) tl[1] = tl_now();)
+            if constexpr (ROPE) {
+                // dims 32s + 8gq + i (s = 0, 1) pair with 64 more (s + 2): the
+                // lane holds both halves of 16 rotation pairs (rope.hip.cpp:44-58)
+                if (qlane && a.apply) {
 #pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    rope_rotate8(qb[s], qb[s + 2], rc[s], rs[s], qb[s], qb[s + 2]);
+                    for (int s = 0; s < 2; ++s)
+                        rope_rotate8(qb[s], qb[s + 2], rc[s], rs[s], qb[s], qb[s + 2]);
+                }
             }
-        }
+        };
 
         const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
 
@@ -409,12 +414,17 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
         // the loads of batch i + 2 go out once batch i is consumed.  Every path
         // into the loop test has exactly batches A and B in flight (the last
         // pair is peeled off below), so the compiler's waits stay vmcnt(16) for
-        // A and let B's loads overlap A's compute.
-        if (!two) {
-            // one batch, nothing issued after it
-            __builtin_amdgcn_sched_barrier(0);
-            compute(A, 0, b, false);
-        } else {
+        // A and let B's loads overlap A's compute.  A wave with one batch
+        // issues no loads past the chunk (their address processing would still
+        // take the CU's load pipeline).  The two forms share no code after
+        // their first loads: with a join between a conditional second batch
+        // and the first batch's use, the compiler's wait for A would have to
+        // cover B as well (the fused RoPE C5 step ran 0.3 us per layer slower).
+        if (b + kStep < nk) {
+            // the first two batches of this wave
+            load(b, A, 0);
+            load(b + kStep, B, 1);
+            rotate_q();
             while (b + 2 * kStep < nk) {
                 __builtin_amdgcn_sched_barrier(0);
                 compute(A, 0, b, true);
@@ -429,6 +439,11 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             // keys past the chunk are masked (p = 0)
             if (b + kStep < nk) compute(B, 1, b + kStep, false);
+        } else {
+            load(b, A, 0);
+            rotate_q();
+            __builtin_amdgcn_sched_barrier(0);
+            compute(A, 0, b, false);
         }
         TL(if (lane == 0) tl[2 + wave] = tl_now();)
     }
