@@ -129,7 +129,8 @@ struct DecodeArgs {
 
 #if defined(ATTN_DECODE_TIMELINE)
 // Record layout of one decode call (64-bit words): split workgroup w at
-// 16 w: [0] entry, [1] first K/V loads issued (wave 0), [2 + wave] that
+// 16 w: [0] entry, [15] wave 0 about to load q, [1] its first K/V loads
+// issued, [2 + wave] that
 // wave's last batch computed (0: the wave had no keys), [14] every wave's
 // state in LDS (after the barrier), [10] thread 0's share of the fold done
 // and its partial stores issued, [11] those stores acknowledged, [12] HW_ID,

@@ -291,6 +291,7 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     // wave-uniform: a wave whose first batch lies past the chunk (short
     // contexts) has no keys and goes straight to the fold
     if (b < nk) {
+        TL(if (tid == 0) tl[15] = tl_now();)
         // Q^T as the B operand: lane (gq, n) holds Q[g*G + n][32s + 8gq .. +7].
         // Q (and the rotation's cos/sin) are loaded before the first K/V batch so
         // that the in-order load counter never makes a batch wait for them.

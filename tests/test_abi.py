@@ -177,6 +177,41 @@ def test_decode_plan_respects_workspace_capacity(attn):
     assert attn.decode_plan(257, 4, 2, 128, kv_stride=2 * 128 + 17)["path"] == 0
 
 
+def test_decode_plan_shapes(attn):
+    """The planner's choices for the SmolLM3 decode shape (16 / 4 heads,
+    D = 128, 256 CUs): one kernel (one split per KV head) up to 384 keys
+    unless decode_whole_max_keys says otherwise; above, one KV head per
+    workgroup and 64 splits up to 12288 keys; two KV heads per workgroup
+    above, with chunks of at least 160 keys while that leaves fewer than 128
+    splits."""
+    p = lambda L: attn.decode_plan(L, 16, 4, 128)  # noqa: E731
+    for L in (1, 16, 17, 100, 254, 384):
+        assert p(L)["nsplit"] == 1 and p(L)["nstate"] == 1 and p(L)["path"] == 3, L
+    assert p(385)["nsplit"] > 1
+    try:
+        attn.set_option("decode_whole_max_keys", -1)
+        assert p(254)["nsplit"] == 16 and p(254)["chunk"] == 16
+        attn.set_option("decode_whole_max_keys", 1000)
+        assert p(1000)["nsplit"] == 1 and p(1001)["nsplit"] > 1
+    finally:
+        attn.set_option("decode_whole_max_keys", 0)
+    # forced split counts or heads per workgroup keep the split plans
+    try:
+        attn.set_option("decode_heads_per_workgroup", 2)
+        assert p(254)["nsplit"] > 1
+    finally:
+        attn.set_option("decode_heads_per_workgroup", 0)
+    assert (p(4096)["path"], p(4096)["nsplit"], p(4096)["chunk"]) == (3, 64, 64)
+    assert (p(16384)["path"], p(16384)["nsplit"], p(16384)["chunk"]) == (2, 103, 160)
+    assert (p(32768)["path"], p(32768)["nsplit"], p(32768)["chunk"]) == (2, 128, 256)
+    assert (p(65536)["path"], p(65536)["nsplit"], p(65536)["chunk"]) == (2, 128, 512)
+    for L in range(12289, 20481, 256):
+        assert p(L)["chunk"] >= 160 and p(L)["nsplit"] <= 128, (L, p(L))
+    # no device work has been captured here: no node records
+    assert attn.lib().attn_graph_node_records() == 0
+    assert attn.lib().attn_set_option(b"graph_node_records", 0) == 0
+
+
 def test_prefill_plan(attn):
     a = 4096
     assert attn.prefill_plan(a, a, a, a, 16, 4, 128, 3072, 512) == 1
