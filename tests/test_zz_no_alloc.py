@@ -26,7 +26,8 @@ def inputs(L, seed):
 
 def test_noalloc_decode_matches_workspace_decode(attn, gpu):
     lib = attn.lib()
-    for L, seed in ((32768, 71), (4096, 72)):
+    # the third call is a one-kernel plan (one split per KV head, no merge)
+    for L, seed in ((32768, 71), (4096, 72), (254, 73)):
         plan = attn.decode_plan(L, HQ, HKV, D)
         print(f"[case] noalloc decode L={L} plan={plan}", flush=True)
         q, k, v = inputs(L, seed)
