@@ -465,10 +465,11 @@ def bench_c5(torch, A, hipgraph, replays, layers=36, L=32769, producer="rope"):
 
 
 def cpu_baselines(torch, quick):
-    """The reference's PyTorch CPU attention (python/reference.py:79-92,
-    fp16 SDPA with repeat_interleave, all torch threads) on a bounded sample
-    of C3 decode calls (~10 s), plus prefill and RoPE samples, and the oracle
-    (fp64 C, 1 thread) on a few decode calls."""
+    """The reference's PyTorch CPU attention (python/reference.py:79-92)
+    restated with the same torch calls (fp16 SDPA with repeat_interleave, all
+    torch threads; kind "port", the reference file is not run) on a bounded
+    sample of C3 decode calls (~10 s), plus prefill and RoPE samples, and the
+    oracle (fp64 C, 1 thread) on a few decode calls."""
     import numpy as np
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
@@ -501,7 +502,7 @@ def cpu_baselines(torch, quick):
     times.sort()
     dt = times[len(times) // 2]
     res["torch_decode"] = {"value": decode_bytes(L) / dt / 1e9, "unit": "GB/s",
-                           "cores": nthreads, "kind": "reference-pytorch",
+                           "cores": nthreads, "kind": "port",
                            "sample": f"torch SDPA fp16 decode, C3 L=32768 (16 q / 4 kv heads, "
                                      f"D=128, K/V repeat_interleave), {len(times)} calls in "
                                      f"{sum(times):.1f} s, median {dt * 1e3:.2f} ms "
@@ -529,7 +530,7 @@ def cpu_baselines(torch, quick):
     dt = float(np.median(times))
     flops = 2 * 4 * D * N * (N + 1)
     res["torch_prefill"] = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": nthreads,
-                            "kind": "reference-pytorch",
+                            "kind": "port",
                             "sample": f"torch SDPA fp16 causal prefill, N={N}, 4 q heads of one "
                                       f"KV group (1/4 of C4), median of 3: {dt:.2f} s"}
     # RoPE as the reference's PyTorch path applies it (python/reference.py:63-73:
@@ -555,7 +556,7 @@ def cpu_baselines(torch, quick):
         times.append(time.perf_counter() - t0)
     dt = float(np.median(times))
     res["torch_rope"] = {"value": rope_bytes(Nr) / dt / 1e9, "unit": "GB/s", "cores": nthreads,
-                         "kind": "reference-pytorch",
+                         "kind": "port",
                          "sample": f"torch fp16 rotate-half RoPE of Q and K, N={Nr} "
                                    f"(algorithmic bytes as the fused kernel), median of 5: "
                                    f"{dt * 1e3:.2f} ms"}
