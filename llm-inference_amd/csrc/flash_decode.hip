@@ -10,10 +10,13 @@
 // workgroup (8 waves) owns one chunk for HPW KV heads (HPW = 1 up to 12288
 // keys, 2 above for SmolLM3); 8/HPW waves share a KV head and each wave
 // serves ALL query heads of its group, so every K/V byte is read from HBM
-// exactly once (the reference reads it once per query head).
+// exactly once (the reference reads it once per query head).  Short
+// contexts (up to kWholeMaxKeys) take one chunk per KV head, and that
+// workgroup's fold writes the output: one kernel (see plan_decode).
 //  * Scores come from v_mfma_f32_16x16x32_f16 as S^T = K . Q^T (keys = rows,
-//    the <= 16 grouped query heads = columns): 16-byte K loads are already
-//    in A-operand layout.  The S^T key rows are permuted so that lane (gq, n)
+//    the <= 16 grouped query heads = columns): K comes in the A-operand
+//    layout either straight from 16-byte loads or, from 4096 keys, through
+//    LDS-DMA of whole 256-byte rows.  The S^T key rows are permuted so that lane (gq, n)
 //    ends up holding query n and keys 8gq..8gq+7 of a 32-key batch, which is
 //    exactly the B-operand layout of P^T for the PV product.
 //  * PV is O^T = V^T . P^T on the same MFMA.  Lane (gq, n) loads 16 B of V
@@ -28,13 +31,15 @@
 //    the end is free.  Each wave keeps two 32-key batches in flight: the
 //    loads of batch i + 2 are issued as soon as batch i has been consumed.
 //  * The waves of a workgroup fold their (max, sum, acc) through LDS into
-//    one unnormalised partial state per query head.
+//    one partial state per query head: fp32 max and sum, and the output
+//    normalised by the sum, in fp16.  A chunk of at most two batches is
+//    taken by one wave per head, which stores its state from registers.
 //
 // Two kernels, as in the reference (attention node + merge node): the split
 // kernel above writes each workgroup's partial states to the caller's
 // workspace, the merge kernel (grid (Hq, D/4), one wave per workgroup) folds
 // every split's partial for 4 output dims of one head: M = max_c m_c,
-// l = sum_c 2^(m_c-M) l_c, out = sum_c 2^(m_c-M) acc_c / l.  The kernel
+// w_c = 2^(m_c-M) l_c, out = sum_c w_c o_c / sum_c w_c.  The kernel
 // boundary orders the partial writes before the merge reads.  Measured and
 // rejected: one kernel holding the split workgroups and merge workgroups
 // (dispatched last) that exchange the partial states through device-coherent
