@@ -94,9 +94,13 @@ def expected(q, k, v, L, Hq=16, Hkv=4, D=128):
     return e32.reshape(-1)
 
 
-@pytest.mark.parametrize("L", [1, 2, 12, 13, 127, 128, 129, 254, 255, 1000, 4096, 16384, 32768,
-                               65536])
+@pytest.mark.parametrize("L", [1, 2, 12, 13, 127, 128, 129, 254, 255, 1000, 3072, 4096, 4097,
+                               12288, 12289, 16384, 20480, 20481, 32768, 32769, 65536])
 def test_decode_smollm3_vs_oracle(attn, gpu, L):
+    # the plan boundaries among them: 64-key chunks taken by one wave (4096)
+    # against LDS-DMA chunks (4097), one against two KV heads per workgroup
+    # (12288 / 12289), 160-key minimum chunks (12289 .. 20480) against 128
+    # splits (20481), an odd chunk with three batches for one wave (32769)
     print(f"[case] decode L={L} plan={attn.decode_plan(L, 16, 4, 128)}", flush=True)
     q, k, v = smol_inputs(L, seed=3)
     got = run_decode(attn, gpu, q, k, v, L, 16, 4, 128)
