@@ -81,11 +81,13 @@ def rand16(torch, n, seed, sigma=1.0, device="cuda"):
     return (torch.randn(n, generator=g, device=device) * sigma).to(torch.float16)
 
 
-def time_graph(torch, A, hipgraph, launch_one, steps, warmup, stream, replays=7):
+def time_graph(torch, A, hipgraph, launch_one, steps, warmup, stream, replays=7,
+               before_replay=None):
     """Warm up with `warmup` eager launches, capture `steps` launches into one
     graph, replay it once untimed, then `replays` times inside event brackets
-    on the launch stream, each bracketed by synchronizations.  Returns ms per
-    launch of the median replay and the (min, median, max) over the
+    on the launch stream, each bracketed by synchronizations (and preceded,
+    outside the brackets, by `before_replay(stream)` when given).  Returns ms
+    per launch of the median replay and the (min, median, max) over the
     replays."""
     sp = stream.cuda_stream
     with torch.cuda.stream(stream):
@@ -103,6 +105,8 @@ def time_graph(torch, A, hipgraph, launch_one, steps, warmup, stream, replays=7)
         for _ in range(replays):
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
+            if before_replay is not None:
+                before_replay(sp)
             torch.cuda.synchronize()
             e0.record(stream)
             hipgraph.launch(exe, sp)
@@ -114,8 +118,30 @@ def time_graph(torch, A, hipgraph, launch_one, steps, warmup, stream, replays=7)
     return times[len(times) // 2], (times[0], times[len(times) // 2], times[-1])
 
 
-def bench_decode(torch, A, hipgraph, L, nbuf, steps, warmup, seed=3):
-    """Flash-Decode over `nbuf` distinct KV buffers in rotation."""
+def cold_buffers(L):
+    """KV buffers a decode at L rotates to be HBM-cold: more than 320 MB
+    together (the MALL holds 256 MB), and at least 8 (C3: 8 x 67 MB)."""
+    return max(8, -(-320_000_000 // decode_bytes(L)))
+
+
+_flush_buf = None
+
+
+def flush_mall(torch, sp):
+    """Reads 512 MB of unrelated device memory on stream `sp`, so that no
+    K/V byte of an earlier replay is still in the MALL (256 MB)."""
+    global _flush_buf
+    if _flush_buf is None:
+        _flush_buf = torch.ones(128 << 20, dtype=torch.int32, device="cuda")
+    n = _flush_buf.numel() * 4 // 2
+    p = _flush_buf.data_ptr()
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    assert bench_lib().attn_bench_read2(p, n, p + n, n, sink.data_ptr(), 1024, sp) == 0
+
+
+def bench_decode(torch, A, hipgraph, L, nbuf, steps, warmup, seed=3, flush=False):
+    """Flash-Decode over `nbuf` distinct KV buffers in rotation (with `flush`,
+    the MALL is flushed before every timed replay)."""
     dev = torch.device("cuda:0")
     q = rand16(torch, Q_DIM, seed)
     ks = [rand16(torch, (L + 1) * KV_DIM, seed + 1 + 2 * b) for b in range(nbuf)]
@@ -132,7 +158,8 @@ def bench_decode(torch, A, hipgraph, L, nbuf, steps, warmup, seed=3):
         assert rc == 0
 
     stream = torch.cuda.Stream()
-    ms, spread = time_graph(torch, A, hipgraph, launch, steps, warmup, stream)
+    ms, spread = time_graph(torch, A, hipgraph, launch, steps, warmup, stream,
+                            before_replay=(lambda sp: flush_mall(torch, sp)) if flush else None)
     del ks, vs
     return ms, spread
 
@@ -167,7 +194,8 @@ def bench_launch_floor(torch, A, hipgraph, kernels, wgs, steps, warmup):
     return time_graph(torch, A, hipgraph, launch, steps, warmup, torch.cuda.Stream())[0]
 
 
-def bench_read_ceiling(torch, A, hipgraph, L, nbuf, steps, warmup, wgs=1024, seed=3):
+def bench_read_ceiling(torch, A, hipgraph, L, nbuf, steps, warmup, wgs=1024, seed=3,
+                       flush=False):
     """A plain streaming read of the same bytes a decode call reads (K and V
     rows 0..L-1 of one of `nbuf` rotated buffers), timed exactly as
     bench_decode times the decode: the ceiling for a decode call."""
@@ -181,7 +209,8 @@ def bench_read_ceiling(torch, A, hipgraph, L, nbuf, steps, warmup, wgs=1024, see
         assert blib.attn_bench_read2(ks[b].data_ptr(), L * KV_DIM * 2, vs[b].data_ptr(),
                                      L * KV_DIM * 2, sink.data_ptr(), wgs, sp) == 0
 
-    ms, spread = time_graph(torch, A, hipgraph, launch, steps, warmup, torch.cuda.Stream())
+    ms, spread = time_graph(torch, A, hipgraph, launch, steps, warmup, torch.cuda.Stream(),
+                            before_replay=(lambda sp: flush_mall(torch, sp)) if flush else None)
     del ks, vs
     return ms, spread
 
@@ -839,10 +868,16 @@ def main():
                                   "launches_us": [t * 1e3 for t in pspread], "launches": 60}}
 
     if not args.quick:
+        # cold from 4096 keys: K/V rotated over more than the MALL holds and
+        # the MALL flushed before each replay; below, the 0.5 MB of C1 stays
+        # in L2/MALL either way (cold = warm)
         for Lx in (254, 4096, 16384, 32768, 65536):
-            nb = 8 if Lx >= 4096 else 1
-            cold, _ = bench_decode(torch, A, hipgraph, Lx, nb, steps, warmup)
+            if Lx >= 4096:
+                cold, _ = bench_decode(torch, A, hipgraph, Lx, cold_buffers(Lx), steps, warmup,
+                                       flush=True)
             warm, _ = bench_decode(torch, A, hipgraph, Lx, 1, steps, warmup)
+            if Lx < 4096:
+                cold = warm
             ent = detail["decode"].setdefault(str(Lx), {})
             ent.update({"cold_us": cold * 1e3, "cold_GBps": decode_bytes(Lx) / cold / 1e6,
                         "warm_us": warm * 1e3, "warm_GBps": decode_bytes(Lx) / warm / 1e6,
@@ -850,7 +885,8 @@ def main():
             log(f"decode L={Lx}: cold {cold * 1e3:.2f} us ({decode_bytes(Lx) / cold / 1e6:.0f} GB/s)"
                 f" warm {warm * 1e3:.2f} us ({decode_bytes(Lx) / warm / 1e6:.0f} GB/s)")
         for Lx in (4096, 65536):
-            r, _ = bench_read_ceiling(torch, A, hipgraph, Lx, 8, steps, warmup)
+            r, _ = bench_read_ceiling(torch, A, hipgraph, Lx, cold_buffers(Lx), steps, warmup,
+                                      flush=True)
             detail["read_ceiling"][str(Lx)] = {"us": r * 1e3, "GBps": decode_bytes(Lx) / r / 1e6}
             log(f"read ceiling L={Lx}: {r * 1e3:.2f} us")
         p254 = bench_prefill_graph(torch, A, hipgraph, 254, steps, warmup)
