@@ -754,12 +754,13 @@ DecodePlan plan_decode(uint32_t kv_len, uint32_t num_heads, uint32_t num_kv_head
     const uint32_t units = (kv_len + unit - 1) / unit;
     const uint32_t cus = (uint32_t)std::max(1, device_cu_count(device));
     const long sopt = get_option(kOptDecodeSplits);
-    // one 8-wave workgroup per CU; with two KV heads per workgroup, chunks of
-    // at least kTwoHeadMinChunk keys even if CUs stay idle (L = 16384: 103
-    // splits of 160 keys 10.30 us, 128 of 128 keys 10.79 us; 14336: 9.86
-    // against 10.19 us; equal or better from 13312 to 19456 keys)
+    // one 8-wave workgroup per CU; with two KV heads per workgroup past
+    // kOneHeadMaxKeys, chunks of at least kTwoHeadMinChunk keys even if CUs
+    // stay idle (L = 16384: 103 splits of 160 keys 10.30 us, 128 of 128 keys
+    // 10.79 us; 14336: 9.86 against 10.19 us; equal or better from 13312 to
+    // 19456 keys; a forced two-head plan on a short context keeps its splits)
     uint32_t target = sopt > 0 ? (uint32_t)sopt : std::max(1u, (cus + groups - 1) / groups);
-    if (sopt <= 0 && hpw == 2)
+    if (sopt <= 0 && hpw == 2 && kv_len > kOneHeadMaxKeys)
         target = std::min(target, std::max(1u, (kv_len + kTwoHeadMinChunk - 1) / kTwoHeadMinChunk));
     uint32_t nsplit = std::max(1u, std::min<uint32_t>({target, units, (uint32_t)kMaxSplits}));
     // at least 16 keys per split: with chunks of >= KV_CHUNK (12) keys the
