@@ -37,8 +37,9 @@
 //
 // Two kernels, as in the reference (attention node + merge node): the split
 // kernel above writes each workgroup's partial states to the caller's
-// workspace, the merge kernel (grid (Hq, D/4), one wave per workgroup) folds
-// every split's partial for 4 output dims of one head: M = max_c m_c,
+// workspace, the merge kernel (grid (Hq, D/8), two waves per workgroup, one
+// per 4 output dims) folds every split's partial for 4 output dims of one
+// head: M = max_c m_c,
 // w_c = 2^(m_c-M) l_c, out = sum_c w_c o_c / sum_c w_c.  The kernel
 // boundary orders the partial writes before the merge reads.  Measured and
 // rejected: one kernel holding the split workgroups and merge workgroups
@@ -585,22 +586,28 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
        })
 }
 
-constexpr int kMergeDims = 4;    // output dims per merge workgroup (one wave)
+constexpr int kMergeDims = 4;    // output dims per merge wave
+// waves per merge workgroup, each on its own 4 dims: C3 14.56 against 14.63
+// us with one wave (512 workgroups), 16384 keys 9.82 against 9.91, 4096 keys
+// 5.93 against 5.98; four waves 14.68 us (same box, alternating builds)
+constexpr int kMergeWaves = 2;
 constexpr int kMergeRound = 4;   // splits per lane per round of loads
 
-// The merge kernel: grid (Hq, D/4), one wave per workgroup.  Lane j
+// The merge kernel: grid (Hq, D/8), two independent waves per workgroup,
+// wave w of workgroup (h, y) on dims 4 (2y + w) .. +3 of head h.  Lane j
 // folds the partials of splits j, j + 64, ... for 4 output dims of one head
 // with an online merge (all loads of a round issued first, through
 // range-checked buffer resources: splits past nstate read as zero and get
 // weight 0); the 64 lanes then combine with DPP moves and lane reads
 // (wave_max, wave_sum).
 template <bool ROPE>
-__global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
-    const uint32_t lane = threadIdx.x;
+__global__ __launch_bounds__(64 * kMergeWaves) void flash_decode_merge(DecodeArgs a) {
+    const uint32_t lane = threadIdx.x & 63u;
     const uint32_t h = blockIdx.x;
-    const uint32_t d0 = blockIdx.y * kMergeDims;
+    const uint32_t dg = blockIdx.y * kMergeWaves + (threadIdx.x >> 6);
+    const uint32_t d0 = dg * kMergeDims;
     const uint32_t S = a.nstate;
-    TL(uint64_t* const tl = a.tl + kTlMergeBase + 4u * (uint64_t)(blockIdx.y * gridDim.x + blockIdx.x);
+    TL(uint64_t* const tl = a.tl + kTlMergeBase + 4u * (uint64_t)(dg * gridDim.x + blockIdx.x);
        if (lane == 0) {
            tl[0] = tl_now();
            tl[3] = tl_xcc_id();
@@ -610,7 +617,7 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
     const BufRsrc rpo = make_rsrc(state_out(a) + (uint64_t)h * S * kD, S * kD * 2u);
     const uint32_t dbyte = d0 * 2u;
     // the rotating lanes fetch the position first, alongside the states
-    const bool rotates = ROPE && a.apply && blockIdx.y < 8 && lane == 0;
+    const bool rotates = ROPE && a.apply && dg < 8 && lane == 0;
     uint32_t row = 0;
     if (rotates) row = __hip_atomic_load(rope_row_word(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
@@ -664,7 +671,7 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
     TL(wait_stores(); if (lane == 0) tl[2] = tl_now();)
     if constexpr (ROPE) {
         // every split workgroup has read q (the kernel boundary orders this)
-        if (rotates) rotate_q_head(a, h, blockIdx.y, row);
+        if (rotates) rotate_q_head(a, h, dg, row);
     }
 }
 
@@ -673,7 +680,7 @@ __global__ __launch_bounds__(64) void flash_decode_merge(DecodeArgs a) {
 // proper tests no flag before its loads (a branch on an argument costs it a
 // kernel-argument round trip of its own, ~0.3 us per call at L = 32768).
 template <bool ROPE>
-__global__ __launch_bounds__(64) void flash_decode_merge_idle(DecodeArgs) {}
+__global__ __launch_bounds__(64 * kMergeWaves) void flash_decode_merge_idle(DecodeArgs) {}
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -820,7 +827,7 @@ dim3 decode_grid(const DecodeArgs& a, const DecodePlan& p) {
 // one workgroup per query head and 4 output dims; one workgroup, which
 // exits at once, for a whole-context plan
 dim3 decode_merge_grid(const DecodeArgs& a) {
-    return a.whole ? dim3(1, 1) : dim3(a.num_heads, kD / kMergeDims);
+    return a.whole ? dim3(1, 1) : dim3(a.num_heads, kD / kMergeDims / kMergeWaves);
 }
 
 #if defined(ATTN_DECODE_TIMELINE)
@@ -867,7 +874,7 @@ hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream, bool rop
     void* args[1] = {const_cast<DecodeArgs*>(&a)};
 #endif
     return hipLaunchKernel(decode_merge_symbol(rope, a.whole != 0), decode_merge_grid(a),
-                           dim3(64), args, 0, stream);
+                           dim3(64 * kMergeWaves), args, 0, stream);
 }
 
 }  // namespace attn
