@@ -57,6 +57,7 @@
 #include "attn_internal.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace attn {
 
@@ -591,7 +592,7 @@ constexpr int kMergeDims = 4;    // output dims per merge wave
 // us with one wave (512 workgroups), 16384 keys 9.82 against 9.91, 4096 keys
 // 5.93 against 5.98; four waves 14.68 us (same box, alternating builds)
 constexpr int kMergeWaves = 2;
-constexpr int kMergeRound = 4;   // splits per lane per round of loads
+constexpr int kMergeRound = 4;   // splits per lane per round of loads past 128 states
 
 // The merge kernel: grid (Hq, D/8), two independent waves per workgroup,
 // wave w of workgroup (h, y) on dims 4 (2y + w) .. +3 of head h.  Lane j
@@ -623,11 +624,13 @@ __global__ __launch_bounds__(64 * kMergeWaves) void flash_decode_merge(DecodeArg
 
     float m = -INFINITY, l = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t base = lane; base < S; base += 64u * kMergeRound) {
-        float mc[kMergeRound], lc[kMergeRound];
-        f16x4 ac[kMergeRound];
+    // one round of loads: states base, base + 64, ..., R of them per lane
+    auto fold_round = [&](uint32_t base, auto r_tag) __attribute__((always_inline)) {
+        constexpr int R = decltype(r_tag)::value;
+        float mc[R], lc[R];
+        f16x4 ac[R];
 #pragma unroll
-        for (int u = 0; u < kMergeRound; ++u) {
+        for (int u = 0; u < R; ++u) {
             const uint32_t c = base + 64u * (uint32_t)u;
             mc[u] = buf_ldf<0>(rpm, c * 4u);
             lc[u] = buf_ldf<0>(rps, c * 4u);
@@ -635,16 +638,16 @@ __global__ __launch_bounds__(64 * kMergeWaves) void flash_decode_merge(DecodeArg
                 f16x4, __builtin_amdgcn_raw_buffer_load_b64(rpo, (int)(c * (kD * 2u) + dbyte), 0, 0));
         }
 #pragma unroll
-        for (int u = 0; u < kMergeRound; ++u)
+        for (int u = 0; u < R; ++u)
             if (base + 64u * (uint32_t)u >= S) mc[u] = -INFINITY;
         float mn = m;
 #pragma unroll
-        for (int u = 0; u < kMergeRound; ++u) mn = fmaxf(mn, mc[u]);  // split `base` is valid
+        for (int u = 0; u < R; ++u) mn = fmaxf(mn, mc[u]);  // split `base` is valid
         const float so = fast_exp2(m - mn);  // first round: 2^-inf = 0
         l *= so;
         acc *= so;
 #pragma unroll
-        for (int u = 0; u < kMergeRound; ++u) {
+        for (int u = 0; u < R; ++u) {
             // state c's weight 2^(m_c - M) l_c times its normalised output
             const float wc = fast_exp2(mc[u] - mn) * lc[u];  // invalid splits: 0
             l += wc;
@@ -652,6 +655,17 @@ __global__ __launch_bounds__(64 * kMergeWaves) void flash_decode_merge(DecodeArg
             for (int e = 0; e < 4; ++e) acc[e] += (float)ac[u][e] * wc;
         }
         m = mn;
+    };
+    // as many loads per lane as the states need, in one round up to 256
+    // states (each load past nstate still takes the address pipeline: rounds
+    // of 4 at 128 states 14.54 against 14.49 us at C3)
+    if (S <= 64u) {
+        if (lane < S) fold_round(lane, std::integral_constant<int, 1>{});
+    } else if (S <= 128u) {
+        fold_round(lane, std::integral_constant<int, 2>{});
+    } else {
+        for (uint32_t base = lane; base < S; base += 64u * kMergeRound)
+            fold_round(base, std::integral_constant<int, kMergeRound>{});
     }
     TL(if (lane == 0) tl[1] = tl_now();)
     // lanes without splits hold m = -inf and get weight 0
