@@ -96,6 +96,42 @@ __device__ __forceinline__ float xor_lane(float v, int mask) {
     return __shfl_xor(v, mask, kWave);
 }
 
+// x and the value of lane i ^ 16 (ROWS = 16) or i ^ 32 (ROWS = 32), in one
+// order or the other, from one VALU lane swap (v_permlane16_swap_b32 /
+// v_permlane32_swap_b32: the odd 16-lane rows of the first operand trade
+// places with the even rows of the second, or the upper half of the first
+// with the lower half of the second) instead of an LDS-unit permute with its
+// ~100 cycles of latency.  The second operand goes through an empty asm so
+// the compiler does not take the two operands, and then the two results,
+// for the same value.
+template <int ROWS>
+__device__ __forceinline__ f32x2 lane_swap_pair(float x) {
+    float y = x;
+    asm volatile("" : "+v"(y));
+    const uint32_t a = __builtin_bit_cast(uint32_t, x), b = __builtin_bit_cast(uint32_t, y);
+    if constexpr (ROWS == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+        return f32x2{__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+    } else {
+        static_assert(ROWS == 32, "lane swaps of 16 or 32 lanes");
+        const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+        return f32x2{__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+    }
+}
+// max / sum of x and lane i ^ MASK's x (MASK 16 or 32); fmaxf and a single
+// fp32 add are commutative, so the results equal fmaxf(x, xor_lane(x, MASK))
+// and x + xor_lane(x, MASK) bit for bit
+template <int MASK>
+__device__ __forceinline__ float max_xor(float x) {
+    const f32x2 p = lane_swap_pair<MASK>(x);
+    return fmaxf(p[0], p[1]);
+}
+template <int MASK>
+__device__ __forceinline__ float add_xor(float x) {
+    const f32x2 p = lane_swap_pair<MASK>(x);
+    return p[0] + p[1];
+}
+
 // Reductions over the 64 lanes of a wave with a uniform result, for a wave
 // whose cross-lane steps sit on its critical path: two DPP quad permutes
 // (xor 1, xor 2) and two DPP row rotations (by 4 and 8 lanes) reduce each

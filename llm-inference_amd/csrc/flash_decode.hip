@@ -394,8 +394,8 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
                     x[4 * tt + i] = v;
                     mx = fmaxf(mx, v);
                 }
-            mx = fmaxf(mx, xor_lane(mx, 16));
-            mx = fmaxf(mx, xor_lane(mx, 32));
+            mx = max_xor<16>(mx);
+            mx = max_xor<32>(mx);
             const float m_new = fmaxf(m_run, mx);
             const float alpha = fast_exp2(m_run - m_new);
             f16x8 pb;
@@ -457,8 +457,8 @@ __global__ __launch_bounds__(512) void flash_decode_split(DecodeArgs a) {
     }
 
     // per-query sum over the four lane groups (the max is already shared)
-    l_run += xor_lane(l_run, 16);
-    l_run += xor_lane(l_run, 32);
+    l_run = add_xor<16>(l_run);
+    l_run = add_xor<32>(l_run);
     // whole-context plans with RoPE: this workgroup is the only reader of
     // its query heads, so once every wave has read them it writes them back
     // rotated, as the merge kernel does otherwise (lanes 0..7 of the phase-0

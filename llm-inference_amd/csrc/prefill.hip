@@ -358,7 +358,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         // m_cur: the block moves them, m_cur and negm to the new m_used.
         if constexpr (kShift) {
             if (__any(mx > thr)) {
-                const float m_tile = fmaxf(mx, xor_lane(mx, 32)) + m_cur;
+                const float m_tile = max_xor<32>(mx) + m_cur;
                 const float mn = (m_tile > m_used + kRescaleSlack) ? m_tile : m_used;
                 const float al = fast_exp2(m_used - mn);
                 l_run *= al;
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
         } else {
             const float m_lane = mx * a.scale_log2;
             if (__any(m_lane > m_used + kRescaleSlack)) {
-                const float m_tile = fmaxf(m_lane, xor_lane(m_lane, 32));
+                const float m_tile = max_xor<32>(m_lane);
                 const float mn = (m_tile > m_used + kRescaleSlack) ? m_tile : m_used;
                 const float al = fast_exp2(m_used - mn);
                 l_run *= al;
@@ -502,7 +502,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
                 for (int i = 0; i < 16; ++i) acc[i] = acc[i] * a1 + ow[i >> 2][i & 3] * a2;
                 m = mx;
             }
-            const float inv = 1.f / (l + xor_lane(l, 32));
+            const float inv = 1.f / add_xor<32>(l);
             const uint32_t query = q0 + n;
             if (query < N) {
                 f16* orow = a.out + ((uint64_t)query * a.num_heads + head) * kD;
@@ -645,7 +645,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
     }
 
     // ---- epilogue: O = O^T / l, packed [N][Hq][D]
-    const float l = l_run + xor_lane(l_run, 32);
+    const float l = add_xor<32>(l_run);
     const float inv = 1.f / l;
     const uint32_t query = q0 + n;
     if (query < N) {
@@ -765,7 +765,7 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
             mx = fmaxf(mx, x);
         }
         // finite: key kv0 <= q0 <= every query of the tile, and kv0 < N
-        mx = fmaxf(mx, xor_lane(mx, 32));
+        mx = max_xor<32>(mx);
         m_unit = mx * a.scale_log2;
         const float mneg = -m_unit;
         const uint32_t grp = (uint32_t)lane >> 4, jl = (uint32_t)lane & 15u;
@@ -800,7 +800,7 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
     }
     const uint32_t query = q0 + n;
     if (last == 0) {
-        const float inv = 1.f / (l_unit + xor_lane(l_unit, 32));
+        const float inv = 1.f / add_xor<32>(l_unit);
         if (query < N) {
             f16* orow = a.out + ((uint64_t)query * a.num_heads + head) * kD;
 #pragma unroll
@@ -846,7 +846,7 @@ __global__ __launch_bounds__(64 * kSkWaves, 1) void prefill_sk32(PrefillArgs a) 
         }
         m = mx;
     }
-    const float inv = 1.f / (l + xor_lane(l, 32));
+    const float inv = 1.f / add_xor<32>(l);
     if (query < N) {
         f16* orow = a.out + ((uint64_t)query * a.num_heads + head) * kD;
 #pragma unroll
@@ -968,7 +968,7 @@ __global__ __launch_bounds__(64 * kSknWaves, 1) void prefill_skn(PrefillArgs a) 
         // the pair's exchange only in the rescale block, as in prefill_d128
         const float m_lane = mx * a.scale_log2;
         if (__any(m_lane > m_used + kRescaleSlack)) {
-            const float m_tile = fmaxf(m_lane, xor_lane(m_lane, 32));
+            const float m_tile = max_xor<32>(m_lane);
             const float mn = (m_tile > m_used + kRescaleSlack) ? m_tile : m_used;
             const float al = fast_exp2(m_used - mn);
             l_run *= al;
@@ -1024,7 +1024,7 @@ __global__ __launch_bounds__(64 * kSknWaves, 1) void prefill_skn(PrefillArgs a) 
 
     const uint32_t query = q0 + n;
     if (last == 0) {
-        const float inv = 1.f / (l_run + xor_lane(l_run, 32));
+        const float inv = 1.f / add_xor<32>(l_run);
         if (query < N) {
             f16* orow = a.out + ((uint64_t)query * a.num_heads + head) * kD;
 #pragma unroll
@@ -1070,7 +1070,7 @@ __global__ __launch_bounds__(64 * kSknWaves, 1) void prefill_skn(PrefillArgs a) 
         for (int i = 0; i < 16; ++i) acc[i] = acc[i] * a1 + ow[i >> 2][i & 3] * a2;
         m = mx;
     }
-    const float inv = 1.f / (l + xor_lane(l, 32));
+    const float inv = 1.f / add_xor<32>(l);
     if (query < N) {
         f16* orow = a.out + ((uint64_t)query * a.num_heads + head) * kD;
 #pragma unroll
