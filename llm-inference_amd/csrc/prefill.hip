@@ -352,7 +352,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void prefill_d128(PrefillArgs a) {
             }
         // lanes n and n + 32 hold one query's keys and share m_used; the
         // pair's maximum exceeds m_used + slack iff one lane's own maximum
-        // does, so the exchange of the two (an LDS round trip) is only made
+        // does, so the exchange of the two (a lane swap) is only made
         // in the rescale block.  One (rarely taken) block rescales, so none of
         // it is speculated into the common path.  The scores are relative to
         // m_cur: the block moves them, m_cur and negm to the new m_used.
