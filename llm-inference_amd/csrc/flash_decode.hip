@@ -600,7 +600,7 @@ constexpr int kMergeRound = 4;   // splits per lane per round of loads past 128 
 // folds the partials of splits j, j + 64, ... for 4 output dims of one head
 // with an online merge (all loads of a round issued first, through
 // range-checked buffer resources: splits past nstate read as zero and get
-// weight 0); the 64 lanes then combine with DPP moves and lane reads
+// weight 0); the 64 lanes then combine with DPP moves and lane swaps
 // (wave_max, wave_sum).
 template <bool ROPE>
 __global__ __launch_bounds__(64 * kMergeWaves) void flash_decode_merge(DecodeArgs a) {

@@ -83,7 +83,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void qkv_gemv(QkvArgs a) {
             acc1 += (float)w1[c] * xc;
         }
     }
-    // wave sums on the VALU (DPP + lane reads): the reduction is the tail of
+    // wave sums on the VALU (DPP + lane swaps): the reduction is the tail of
     // every row pair's critical path
     acc0 = wave_sum(acc0);
     acc1 = wave_sum(acc1);
